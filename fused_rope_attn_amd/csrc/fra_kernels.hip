@@ -1,0 +1,781 @@
+// fra_kernels.hip -- gfx950 kernels of the fused RoPE + varlen attention path.
+//
+// Two kernel families replace the reference's single Triton kernel
+// (reference fused_attn.py:235-423):
+//
+//   window_kernel  every segment has <= 64 tokens (Qwen2.5-VL window layers).
+//                  One wavefront owns one (segment, head): it loads Q and K
+//                  rows straight into MFMA operand registers, rotates them in
+//                  fp32 there, stages V transposed in LDS, and does one
+//                  64x64 softmax -- no online rescaling is needed.
+//   long_kernel    segments of any length (full-attention layers).  Split-Q
+//                  flash tiling: a 4-wave workgroup owns 128 query rows of one
+//                  (segment, head); K is rotated once per 64-row block while
+//                  it is staged in LDS, V is staged transposed, and each wave
+//                  runs an exp2 online softmax over its 32 rows.
+//
+// Matrix products use v_mfma_f32_32x32x16_{bf16,f16}.  Scores are computed
+// transposed (S^T = K_rot Q_rot^T) so that the 32x32 accumulator layout puts
+// one query per lane column: row max and row sum are in-lane reductions plus
+// one exchange with lane^32, and P^T is already in the B-operand layout of the
+// PV product O^T = V^T P^T.
+//
+// The contraction index of QK^T may be visited in any order as long as Q and
+// K use the same one.  The window kernel feeds k-slot group g (lanes 32g..)
+// of MFMA step t with {x0r[4i..4i+3], x1r[4i..4i+3]} for quad i = g*S + t, so
+// each lane rotates only the quads it feeds (no redundant loads).  The long
+// kernel keeps K_rot in LDS in natural order [x0r | x1r | 0-pad].
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "fra.h"
+
+namespace {
+
+typedef uint32_t u32;
+typedef uint16_t u16;
+typedef __attribute__((__vector_size__(2 * sizeof(u32)))) u32 u32x2;
+typedef __attribute__((__vector_size__(4 * sizeof(u32)))) u32 u32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_inff();
+
+// Kernel parameters, passed by value.  Strides are in elements.
+struct KParams {
+    const char *q, *k, *v, *cos, *sin;
+    char *out;
+    const int32_t *cu;
+    int64_t sq_s, sq_h, sk_s, sk_h, sv_s, sv_h, so_s, so_h, sr_s;
+    int32_t total, num_heads, num_seqs, max_seqlen;
+    int32_t qblocks;      // long kernel: query blocks per (segment, head)
+    float scale_log2;     // softmax_scale * log2(e)
+};
+
+// ---- element traits ---------------------------------------------------------
+
+struct BF16 {
+    static __device__ __forceinline__ float lo(u32 w) { return __builtin_bit_cast(float, w << 16); }
+    static __device__ __forceinline__ float hi(u32 w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+    static __device__ __forceinline__ u32 pack(float a, float b) {
+        bf16x2 v = {(__bf16)a, (__bf16)b};  // v_cvt_pk_bf16_f32, round to nearest even
+        return __builtin_bit_cast(u32, v);
+    }
+    static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                      __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+};
+
+struct F16 {
+    static __device__ __forceinline__ float lo(u32 w) {
+        return (float)__builtin_bit_cast(_Float16, (u16)(w & 0xffffu));
+    }
+    static __device__ __forceinline__ float hi(u32 w) {
+        return (float)__builtin_bit_cast(_Float16, (u16)(w >> 16));
+    }
+    static __device__ __forceinline__ u32 pack(float a, float b) {
+        f16x2 v = {(_Float16)a, (_Float16)b};  // round to nearest even
+        return __builtin_bit_cast(u32, v);
+    }
+    static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                     __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+};
+
+// cos/sin table element types: a quad (4 consecutive entries) as fp32.
+template <int RD> struct Rope;
+template <> struct Rope<FRA_DTYPE_F32> {
+    static constexpr int kBytes = 4;
+    static __device__ __forceinline__ f32x4 quad(const char *p) { return *(const f32x4 *)p; }
+};
+template <> struct Rope<FRA_DTYPE_BF16> {
+    static constexpr int kBytes = 2;
+    static __device__ __forceinline__ f32x4 quad(const char *p) {
+        u32x2 w = *(const u32x2 *)p;
+        return f32x4{BF16::lo(w[0]), BF16::hi(w[0]), BF16::lo(w[1]), BF16::hi(w[1])};
+    }
+};
+template <> struct Rope<FRA_DTYPE_F16> {
+    static constexpr int kBytes = 2;
+    static __device__ __forceinline__ f32x4 quad(const char *p) {
+        u32x2 w = *(const u32x2 *)p;
+        return f32x4{F16::lo(w[0]), F16::hi(w[0]), F16::lo(w[1]), F16::hi(w[1])};
+    }
+};
+
+// ---- small helpers ------------------------------------------------------------
+
+// Consecutive logical units on the same XCD.  Workgroup b is dispatched to
+// XCD b % 8; this bijection on [0, n) gives XCD x the contiguous range of
+// units [x*ceil, ...), so units that share cache lines (adjacent heads of a
+// window, the query blocks of one head) share one L2.
+__device__ __forceinline__ int xcd_remap(int b, int n) {
+    constexpr int kXcd = 8;
+    const int xcd = b % kXcd, local = b / kXcd;
+    const int base = n / kXcd, rem = n % kXcd;
+    return xcd < rem ? xcd * (base + 1) + local : rem * (base + 1) + (xcd - rem) * base + local;
+}
+
+// Value held by lane (lane ^ 32).
+__device__ __forceinline__ float xchg32(float x) {
+    const int lane = threadIdx.x & 63;
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, x)));
+}
+
+__device__ __forceinline__ u32 perm(u32 hi_src, u32 lo_src, u32 sel) {
+    return __builtin_amdgcn_perm(hi_src, lo_src, sel);
+}
+constexpr u32 kSelLo = 0x05040100u;  // {lo16(lo_src), lo16(hi_src)}
+constexpr u32 kSelHi = 0x07060302u;  // {hi16(lo_src), hi16(hi_src)}
+
+// Split-half rotation of one quad pair, in fp32 with separately rounded
+// products (reference fused_attn.py:340-345 and :385-390; the same order of
+// roundings as the unfused torch path), packed to the storage dtype.
+template <class E>
+__device__ __forceinline__ void rotate_quad(u32x2 x0w, u32x2 x1w, f32x4 c0, f32x4 s0, f32x4 c1, f32x4 s1,
+                                            u32x2 &r0w, u32x2 &r1w) {
+#pragma clang fp contract(off)
+    const float x0[4] = {E::lo(x0w[0]), E::hi(x0w[0]), E::lo(x0w[1]), E::hi(x0w[1])};
+    const float x1[4] = {E::lo(x1w[0]), E::hi(x1w[0]), E::lo(x1w[1]), E::hi(x1w[1])};
+    float r0[4], r1[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r0[i] = x0[i] * c0[i] - x1[i] * s0[i];
+        r1[i] = x0[i] * s1[i] + x1[i] * c1[i];
+    }
+    r0w = u32x2{E::pack(r0[0], r0[1]), E::pack(r0[2], r0[3])};
+    r1w = u32x2{E::pack(r1[0], r1[1]), E::pack(r1[2], r1[3])};
+}
+
+// Loads quad i (entries 4i..4i+3) of both halves of one x row and of the
+// matching cos/sin rows, and rotates it.  The loads are unconditional -- the
+// caller passes pointers that are valid for every lane (rows clamped into the
+// segment) -- so the load stream stays one straight-line block; `valid` false
+// zeroes the result.  FULL selects tables of width D (second half used for
+// x1', the HF layout) over width D/2 (the reference layout).
+template <int D, class E, int RD, bool FULL>
+__device__ __forceinline__ void load_rotate_quad(const char *xrow, const char *crow, const char *srow, int i,
+                                                 bool valid, u32x2 &r0w, u32x2 &r1w) {
+    constexpr int HALF = D / 2;
+    constexpr int RB = Rope<RD>::kBytes;
+    u32x2 x0 = *(const u32x2 *)(xrow + 8 * i);
+    u32x2 x1 = *(const u32x2 *)(xrow + 2 * HALF + 8 * i);
+    const f32x4 c0 = Rope<RD>::quad(crow + RB * 4 * i);
+    const f32x4 s0 = Rope<RD>::quad(srow + RB * 4 * i);
+    f32x4 c1 = c0, s1 = s0;
+    if constexpr (FULL) {
+        c1 = Rope<RD>::quad(crow + RB * (HALF + 4 * i));
+        s1 = Rope<RD>::quad(srow + RB * (HALF + 4 * i));
+    }
+    if (!valid) {
+        x0 = u32x2{0u, 0u};
+        x1 = u32x2{0u, 0u};
+    }
+    rotate_quad<E>(x0, x1, c0, s0, c1, s1, r0w, r1w);
+}
+
+// ---- window kernel ------------------------------------------------------------
+//
+// One wavefront per (segment, head), segment length L <= 64.  Lane (r, g)
+// (r = lane & 31, g = lane >> 5) holds the operands of tokens r and r + 32:
+// K_rot rows as the A operand of S^T and Q_rot rows as its B operand.
+
+template <int D, class E, int RD, bool FULL>
+__global__ __launch_bounds__(64, 3) void window_kernel(const KParams p) {
+    constexpr int HALF = D / 2;
+    constexpr int NQ = D / 8;           // quads per half
+    constexpr int S = (NQ + 1) / 2;     // 16-deep k-steps of QK^T
+    constexpr int NCH = D / 8;          // 16-byte chunks per V row
+    constexpr int CH0 = (NCH + 1) / 2;  // chunks staged by lane group 0
+    constexpr int NDT = (D + 31) / 32;  // 32-row tiles of O^T
+    constexpr int VTS = 34;             // dwords per V^T row: 32 kv pairs + 2 pad
+    constexpr int VROWS = 16 * CH0;     // staged rows incl. the scratch rows of a missing odd chunk
+    __shared__ u32 vt[VROWS * VTS];
+
+    const int lane = threadIdx.x;
+    const int r = lane & 31, g = lane >> 5;
+    const int u = xcd_remap(blockIdx.x, gridDim.x);
+    const int seg = u / p.num_heads, head = u - seg * p.num_heads;
+    int s0 = p.cu[seg], s1 = p.cu[seg + 1];
+    s0 = min(max(s0, 0), p.total);
+    s1 = min(max(s1, 0), p.total);
+    const int L = min(s1 - s0, 64);
+    if (L <= 0) return;
+
+    // V^T staging: lane (r, g) packs kv rows 2r and 2r+1 for chunks
+    // [g*CH0, g*CH0 + CH0); vt[d][r] holds {V[2r][d], V[2r+1][d]}.  Rows
+    // past the segment are read at its first row and zeroed; a chunk index
+    // past the row (odd NCH) reads chunk 0 and lands in scratch rows >= D.
+    {
+        const int ra = 2 * r, rb = 2 * r + 1;
+        const bool va = ra < L, vb = rb < L;
+        const int64_t hoff = (int64_t)head * p.sv_h;
+        const char *pa = p.v + ((int64_t)(s0 + (va ? ra : 0)) * p.sv_s + hoff) * 2;
+        const char *pb = p.v + ((int64_t)(s0 + (vb ? rb : 0)) * p.sv_s + hoff) * 2;
+        u32x4 A[CH0], B[CH0];
+#pragma unroll
+        for (int cc = 0; cc < CH0; ++cc) {
+            const int c = g * CH0 + cc;
+            const int cl = c < NCH ? c : 0;
+            A[cc] = *(const u32x4 *)(pa + 16 * cl);
+            B[cc] = *(const u32x4 *)(pb + 16 * cl);
+        }
+#pragma unroll
+        for (int cc = 0; cc < CH0; ++cc) {
+            const int c = g * CH0 + cc;
+            if (!va) A[cc] = u32x4{0u, 0u, 0u, 0u};
+            if (!vb) B[cc] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                vt[(8 * c + 2 * j) * VTS + r] = perm(B[cc][j], A[cc][j], kSelLo);
+                vt[(8 * c + 2 * j + 1) * VTS + r] = perm(B[cc][j], A[cc][j], kSelHi);
+            }
+        }
+    }
+
+    // Q_rot / K_rot operands in registers.
+    u32x4 qop[2][S], kop[2][S];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int tok = r + 32 * tt;
+        const bool valid = tok < L;
+        const int64_t row = s0 + (valid ? tok : 0);
+        const char *qrow = p.q + (row * p.sq_s + (int64_t)head * p.sq_h) * 2;
+        const char *krow = p.k + (row * p.sk_s + (int64_t)head * p.sk_h) * 2;
+        const char *crow = p.cos + row * p.sr_s * Rope<RD>::kBytes;
+        const char *srow = p.sin + row * p.sr_s * Rope<RD>::kBytes;
+#pragma unroll
+        for (int t = 0; t < S; ++t) {
+            const int i = g * S + t;
+            const bool has = valid && i < NQ;
+            const int il = i < NQ ? i : 0;
+            u32x2 a0, a1, b0, b1;
+            load_rotate_quad<D, E, RD, FULL>(qrow, crow, srow, il, has, a0, a1);
+            load_rotate_quad<D, E, RD, FULL>(krow, crow, srow, il, has, b0, b1);
+            qop[tt][t] = u32x4{a0[0], a0[1], a1[0], a1[1]};
+            kop[tt][t] = u32x4{b0[0], b0[1], b1[0], b1[1]};
+        }
+    }
+    __syncthreads();
+
+    const float sl = p.scale_log2;
+    const int nkt = (L + 31) >> 5;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        if (b * 32 >= L) break;
+        // S^T tiles: rows kv, columns q.  Lane (r, g) holds q = 32b + r and
+        // kv = 32a + 8(j/4) + 4g + (j%4) in element j of sacc[a].
+        f32x16 sacc[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            sacc[a] = f32x16{};
+            if (a < nkt) {
+#pragma unroll
+                for (int t = 0; t < S; ++t) sacc[a] = E::mma(kop[a][t], qop[b][t], sacc[a]);
+            }
+        }
+        float mx = kNegInf;
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int kv = 32 * a + 8 * (j >> 2) + 4 * g + (j & 3);
+                if (kv >= L) sacc[a][j] = kNegInf;
+                mx = fmaxf(mx, sacc[a][j]);
+            }
+        }
+        mx = fmaxf(mx, xchg32(mx));
+        const float mneg = -mx * sl;
+        float lsum = 0.f;
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[a][j], sl, mneg));
+                sacc[a][j] = e;
+                lsum += e;
+            }
+        }
+        lsum += xchg32(lsum);
+
+        // P^T as the B operand of O^T = V^T P^T: step (a, h) uses elements
+        // 8h..8h+7 of sacc[a], i.e. kv = 32a + 16h + {4g..4g+3, 8+4g..8+4g+3}.
+        u32x4 pop[2][2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                pop[a][h] = u32x4{E::pack(sacc[a][8 * h + 0], sacc[a][8 * h + 1]),
+                                  E::pack(sacc[a][8 * h + 2], sacc[a][8 * h + 3]),
+                                  E::pack(sacc[a][8 * h + 4], sacc[a][8 * h + 5]),
+                                  E::pack(sacc[a][8 * h + 6], sacc[a][8 * h + 7])};
+        }
+
+        // One 32-row d tile of O^T at a time, stored as soon as it is done.
+        // Element j of oacc: q = 32b + r, d = 32dt + 8(j/4) + 4g + (j%4).
+        const int q = 32 * b + r;
+        const float inv = 1.0f / lsum;
+        char *orow = p.out + ((int64_t)(s0 + q) * p.so_s + (int64_t)head * p.so_h) * 2;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            const int d = 32 * dt + r;
+            const u32 *vrow = vt + min(d, D - 1) * VTS + 2 * g;
+            f32x16 oacc = f32x16{};
+#pragma unroll
+            for (int a = 0; a < 2; ++a) {
+                if (a >= nkt) break;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int kvh = 16 * a + 8 * h;  // dword column of kv = 32a + 16h + 4g, minus 2g
+                    const u32x2 lo = *(const u32x2 *)(vrow + kvh);
+                    const u32x2 hi = *(const u32x2 *)(vrow + kvh + 4);
+                    u32x4 vop = {lo[0], lo[1], hi[0], hi[1]};
+                    if (d >= D) vop = u32x4{0u, 0u, 0u, 0u};
+                    oacc = E::mma(vop, pop[a][h], oacc);
+                }
+            }
+            if (q < L) {
+#pragma unroll
+                for (int jq = 0; jq < 4; ++jq) {
+                    const int d0 = 32 * dt + 8 * jq + 4 * g;
+                    if (d0 < D) {
+                        const u32x2 w = {E::pack(oacc[4 * jq + 0] * inv, oacc[4 * jq + 1] * inv),
+                                         E::pack(oacc[4 * jq + 2] * inv, oacc[4 * jq + 3] * inv)};
+                        *(u32x2 *)(orow + 2 * d0) = w;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---- long kernel ----------------------------------------------------------------
+
+constexpr int kLongBQ = 128;   // query rows per workgroup (4 waves x 32)
+constexpr int kLongBKV = 64;   // key/value rows per LDS stage
+constexpr int kLongThreads = 256;
+
+template <int D> struct LongLds {
+    static constexpr int DP = (D + 15) / 16 * 16;      // K_rot row padded to the MFMA k-step
+    static constexpr int KS = DP + 8;                  // K_rot row stride (elements), 16 B pad
+    static constexpr int NDT = (D + 31) / 32;
+    static constexpr int VTS = 36;                     // V^T row stride (dwords): 32 kv pairs + 4 pad
+    static constexpr int kBytes = kLongBKV * KS * 2 + NDT * 32 * VTS * 4;
+};
+
+template <int D, class E, int RD, bool FULL>
+__global__ __launch_bounds__(kLongThreads) void long_kernel(const KParams p) {
+    constexpr int HALF = D / 2;
+    constexpr int NQ = D / 8;
+    constexpr int DP = LongLds<D>::DP;
+    constexpr int S = DP / 16;
+    constexpr int KS = LongLds<D>::KS;
+    constexpr int NDT = LongLds<D>::NDT;
+    constexpr int VTS = LongLds<D>::VTS;
+    constexpr int NCH = D / 8;
+    __shared__ __attribute__((aligned(16))) u16 ks[kLongBKV * KS];
+    __shared__ __attribute__((aligned(16))) u32 vt[NDT * 32 * VTS];
+
+    const int u = xcd_remap(blockIdx.x, gridDim.x);
+    const int sh = u / p.qblocks, qblk = u - sh * p.qblocks;
+    const int seg = sh / p.num_heads, head = sh - seg * p.num_heads;
+    int s0 = p.cu[seg], s1 = p.cu[seg + 1];
+    s0 = min(max(s0, 0), p.total);
+    s1 = min(max(s1, 0), p.total);
+    const int L = s1 - s0;
+    if (L <= 0 || qblk * kLongBQ >= L) return;  // uniform across the workgroup
+
+    const int tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63;
+    const int r = lane & 31, g = lane >> 5;
+
+    // Zero the K_rot pad columns [D, DP) and the V^T pad rows [D, 32*NDT):
+    // staging never writes them.
+    for (int i = tid; i < kLongBKV * (KS - D); i += kLongThreads) {
+        const int row = i / (KS - D), col = D + i % (KS - D);
+        ks[row * KS + col] = 0;
+    }
+    for (int i = tid; i < (NDT * 32 - D) * VTS; i += kLongThreads) vt[D * VTS + i] = 0u;
+
+    // Q_rot of this lane's query row, natural order [x0r | x1r | 0], as the
+    // B operand of S^T: step t, group g takes elements 16t + 8g .. +7.
+    u32x4 qop[S];
+    {
+        const int q = qblk * kLongBQ + 32 * w + r;
+        const bool valid = q < L;
+        const int64_t row = s0 + (valid ? q : 0);
+        const char *qrow = p.q + (row * p.sq_s + (int64_t)head * p.sq_h) * 2;
+        const char *crow = p.cos + row * p.sr_s * Rope<RD>::kBytes;
+        const char *srow = p.sin + row * p.sr_s * Rope<RD>::kBytes;
+        u32x2 nat[DP / 4];  // natural quads: 0..NQ-1 = x0r, NQ..2NQ-1 = x1r, rest 0
+#pragma unroll
+        for (int i = 0; i < NQ; ++i)
+            load_rotate_quad<D, E, RD, FULL>(qrow, crow, srow, i, valid, nat[i], nat[NQ + i]);
+#pragma unroll
+        for (int i = 2 * NQ; i < DP / 4; ++i) nat[i] = u32x2{0u, 0u};
+#pragma unroll
+        for (int t = 0; t < S; ++t) {
+            const u32x2 a = g ? nat[4 * t + 2] : nat[4 * t];
+            const u32x2 b = g ? nat[4 * t + 3] : nat[4 * t + 1];
+            qop[t] = u32x4{a[0], a[1], b[0], b[1]};
+        }
+    }
+
+    const float sl = p.scale_log2;
+    float m_i = kNegInf, l_i = 0.f;
+    f32x16 oacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = f32x16{};
+
+    for (int kb = 0; kb < L; kb += kLongBKV) {
+        __syncthreads();  // the previous block's operands have been read
+        // Stage K_rot: item (row, quad i) rotates quad i of both halves.
+        for (int it = tid; it < kLongBKV * NQ; it += kLongThreads) {
+            const int row = it / NQ, i = it - row * NQ;
+            const int tok = kb + row;
+            const bool valid = tok < L;
+            const int64_t grow = s0 + (valid ? tok : 0);
+            const char *krow = p.k + (grow * p.sk_s + (int64_t)head * p.sk_h) * 2;
+            const char *crow = p.cos + grow * p.sr_s * Rope<RD>::kBytes;
+            const char *srow = p.sin + grow * p.sr_s * Rope<RD>::kBytes;
+            u32x2 r0w, r1w;
+            load_rotate_quad<D, E, RD, FULL>(krow, crow, srow, i, valid, r0w, r1w);
+            *(u32x2 *)(ks + row * KS + 4 * i) = r0w;
+            *(u32x2 *)(ks + row * KS + HALF + 4 * i) = r1w;
+        }
+        // Stage V^T: item (kv quad, 16-byte chunk c); vt[d][2kq..2kq+1]
+        // holds V[4kq..4kq+3][d].
+        for (int it = tid; it < (kLongBKV / 4) * NCH; it += kLongThreads) {
+            const int kq = it / NCH, c = it - kq * NCH;
+            u32x4 x[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int tok = kb + 4 * kq + e;
+                const bool valid = tok < L;
+                x[e] = *(const u32x4 *)(p.v + ((int64_t)(s0 + (valid ? tok : 0)) * p.sv_s + (int64_t)head * p.sv_h) * 2 +
+                                        16 * c);
+                if (!valid) x[e] = u32x4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                *(u32x2 *)(vt + (8 * c + 2 * j) * VTS + 2 * kq) =
+                    u32x2{perm(x[1][j], x[0][j], kSelLo), perm(x[3][j], x[2][j], kSelLo)};
+                *(u32x2 *)(vt + (8 * c + 2 * j + 1) * VTS + 2 * kq) =
+                    u32x2{perm(x[1][j], x[0][j], kSelHi), perm(x[3][j], x[2][j], kSelHi)};
+            }
+        }
+        __syncthreads();
+
+        const int nkv = min(kLongBKV, L - kb);
+        const int nkt = (nkv + 31) >> 5;
+        f32x16 sacc[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            sacc[a] = f32x16{};
+            if (a < nkt) {
+                const u16 *krow = ks + (32 * a + r) * KS + 8 * g;
+#pragma unroll
+                for (int t = 0; t < S; ++t)
+                    sacc[a] = E::mma(*(const u32x4 *)(krow + 16 * t), qop[t], sacc[a]);
+            }
+        }
+        float mx = kNegInf;
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int kv = 32 * a + 8 * (j >> 2) + 4 * g + (j & 3);
+                if (kv >= nkv) sacc[a][j] = kNegInf;
+                mx = fmaxf(mx, sacc[a][j]);
+            }
+        }
+        mx = fmaxf(mx, xchg32(mx));
+        const float m_new = fmaxf(m_i, mx * sl);
+        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+        float lsum = 0.f;
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[a][j], sl, -m_new));
+                sacc[a][j] = e;
+                lsum += e;
+            }
+        }
+        lsum += xchg32(lsum);
+        l_i = l_i * alpha + lsum;
+        m_i = m_new;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
+
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            if (a >= nkt) break;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const u32x4 pop = {E::pack(sacc[a][8 * h + 0], sacc[a][8 * h + 1]),
+                                   E::pack(sacc[a][8 * h + 2], sacc[a][8 * h + 3]),
+                                   E::pack(sacc[a][8 * h + 4], sacc[a][8 * h + 5]),
+                                   E::pack(sacc[a][8 * h + 6], sacc[a][8 * h + 7])};
+                const int kvh = 16 * a + 8 * h + 2 * g;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    const u32 *vrow = vt + (32 * dt + r) * VTS + kvh;
+                    const u32x2 lo = *(const u32x2 *)(vrow);
+                    const u32x2 hi = *(const u32x2 *)(vrow + 4);
+                    oacc[dt] = E::mma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pop, oacc[dt]);
+                }
+            }
+        }
+    }
+
+    const int q = qblk * kLongBQ + 32 * w + r;
+    if (q < L) {
+        const float inv = 1.0f / l_i;
+        char *orow = p.out + ((int64_t)(s0 + q) * p.so_s + (int64_t)head * p.so_h) * 2;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq) {
+                const int d0 = 32 * dt + 8 * jq + 4 * g;
+                if (d0 < D) {
+                    const u32x2 wv = {E::pack(oacc[dt][4 * jq + 0] * inv, oacc[dt][4 * jq + 1] * inv),
+                                      E::pack(oacc[dt][4 * jq + 2] * inv, oacc[dt][4 * jq + 3] * inv)};
+                    *(u32x2 *)(orow + 2 * d0) = wv;
+                }
+            }
+        }
+    }
+}
+
+// ---- host-side dispatch ---------------------------------------------------------
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+typedef void (*KernelFn)(KParams);
+
+// The window kernel keeps the Q_rot and K_rot operands of 64 tokens in
+// registers; above this head_dim the long kernel serves short segments too.
+constexpr int kWindowMaxD = 96;
+
+struct Choice {
+    KernelFn fn;
+    int kernel, grid, block, block_q, block_kv, lds;
+    char name[64];
+};
+
+template <int D, class E, int RD, bool FULL> void pick_full(bool window, Choice &c) {
+    if constexpr (D <= kWindowMaxD) {
+        c.fn = window ? (KernelFn)window_kernel<D, E, RD, FULL> : (KernelFn)long_kernel<D, E, RD, FULL>;
+    } else {
+        c.fn = (KernelFn)long_kernel<D, E, RD, FULL>;
+    }
+}
+
+template <int D, class E, int RD> void pick_rd(bool window, bool full, Choice &c) {
+    if (full) pick_full<D, E, RD, true>(window, c);
+    else pick_full<D, E, RD, false>(window, c);
+}
+
+template <int D> bool pick_d(bool window, bool full, int qkv, int rd, Choice &c) {
+    if (qkv == FRA_DTYPE_BF16) {
+        if (rd == FRA_DTYPE_F32) pick_rd<D, BF16, FRA_DTYPE_F32>(window, full, c);
+        else if (rd == FRA_DTYPE_BF16) pick_rd<D, BF16, FRA_DTYPE_BF16>(window, full, c);
+        else pick_rd<D, BF16, FRA_DTYPE_F16>(window, full, c);
+    } else {
+        if (rd == FRA_DTYPE_F32) pick_rd<D, F16, FRA_DTYPE_F32>(window, full, c);
+        else if (rd == FRA_DTYPE_BF16) pick_rd<D, F16, FRA_DTYPE_BF16>(window, full, c);
+        else pick_rd<D, F16, FRA_DTYPE_F16>(window, full, c);
+    }
+    if (window) {
+        c.lds = 16 * ((D / 8 + 1) / 2) * 34 * 4;
+    } else {
+        c.lds = LongLds<D>::kBytes;
+    }
+    return true;
+}
+
+// Head dims with compiled kernels.  Each must be a multiple of 8 so that
+// both halves of a row start on an 8-byte boundary.
+bool pick_kernel(int d, bool window, bool full, int qkv, int rd, Choice &c) {
+    switch (d) {
+        case 64: return pick_d<64>(window, full, qkv, rd, c);
+        case 72: return pick_d<72>(window, full, qkv, rd, c);
+        case 80: return pick_d<80>(window, full, qkv, rd, c);
+        case 96: return pick_d<96>(window, full, qkv, rd, c);
+        case 128: return pick_d<128>(window, full, qkv, rd, c);
+        default: return false;
+    }
+}
+
+bool aligned(const void *ptr, int bytes) { return ((uintptr_t)ptr % (uintptr_t)bytes) == 0; }
+
+const char *dtype_name(int dt) {
+    switch (dt) {
+        case FRA_DTYPE_BF16: return "bf16";
+        case FRA_DTYPE_F16: return "f16";
+        case FRA_DTYPE_F32: return "f32";
+        default: return "?";
+    }
+}
+
+int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
+    if (!a) return fail(FRA_EINVAL, "args is NULL");
+    if (a->flags != 0) return fail(FRA_EINVAL, "flags must be 0, got %d", a->flags);
+    if (a->num_heads <= 0) return fail(FRA_EINVAL, "num_heads must be positive, got %d", a->num_heads);
+    if (a->head_dim <= 0 || a->head_dim % 2 != 0)
+        return fail(FRA_EINVAL, "head_dim must be positive and even, got %d", a->head_dim);
+    if (a->total_seq < 0) return fail(FRA_EINVAL, "total_seq must be >= 0, got %d", a->total_seq);
+    if (a->num_seqs < 1) return fail(FRA_EINVAL, "num_seqs must be >= 1, got %d", a->num_seqs);
+    if (a->max_seqlen < 1) return fail(FRA_EINVAL, "max_seqlen must be >= 1, got %d", a->max_seqlen);
+    if (a->qkv_dtype != FRA_DTYPE_BF16 && a->qkv_dtype != FRA_DTYPE_F16)
+        return fail(FRA_EINVAL, "qkv_dtype must be bf16 or f16, got %d", a->qkv_dtype);
+    if (a->rope_dtype != FRA_DTYPE_F32 && a->rope_dtype != FRA_DTYPE_BF16 && a->rope_dtype != FRA_DTYPE_F16)
+        return fail(FRA_EINVAL, "rope_dtype must be f32, bf16 or f16, got %d", a->rope_dtype);
+    const int d = a->head_dim;
+    if (a->rope_width != d / 2 && a->rope_width != d)
+        return fail(FRA_EINVAL, "rope_width must be head_dim/2=%d or head_dim=%d, got %d", d / 2, d, a->rope_width);
+    if (!(a->softmax_scale > 0.f) || a->softmax_scale == __builtin_inff())
+        return fail(FRA_EINVAL, "softmax_scale must be finite and > 0, got %g", (double)a->softmax_scale);
+    if (!a->q || !a->k || !a->v || !a->cos || !a->sin || !a->out || !a->cu_seqlens)
+        return fail(FRA_EINVAL, "a tensor pointer is NULL");
+    const int64_t strides[9] = {a->q_stride_seq, a->q_stride_head, a->k_stride_seq, a->k_stride_head,
+                                a->v_stride_seq, a->v_stride_head, a->out_stride_seq, a->out_stride_head,
+                                a->rope_stride_seq};
+    for (int i = 0; i < 9; ++i)
+        if (strides[i] < 0) return fail(FRA_EINVAL, "strides must be >= 0");
+
+    const bool window = a->max_seqlen <= 64 && d <= kWindowMaxD;
+    memset(&c, 0, sizeof(c));
+    if (!pick_kernel(d, window, a->rope_width == d, a->qkv_dtype, a->rope_dtype, c))
+        return fail(FRA_EUNSUPPORTED, "head_dim=%d has no compiled kernel (built: 64, 72, 80, 96, 128)", d);
+
+    // Alignment: Q/K/out are read/written in 8-byte quads, V in 16-byte
+    // chunks, fp32 tables in 16-byte quads and 16-bit tables in 8-byte quads.
+    const int re = a->rope_dtype == FRA_DTYPE_F32 ? 4 : 2;
+    if (!aligned(a->q, 8) || !aligned(a->k, 8) || !aligned(a->out, 8) || !aligned(a->v, 16) ||
+        !aligned(a->cos, 4 * re) || !aligned(a->sin, 4 * re))
+        return fail(FRA_EUNSUPPORTED, "tensor base pointers are not aligned (q/k/out 8 B, v 16 B, cos/sin %d B)", 4 * re);
+    if (a->q_stride_seq % 4 || a->q_stride_head % 4 || a->k_stride_seq % 4 || a->k_stride_head % 4 ||
+        a->out_stride_seq % 4 || a->out_stride_head % 4 || a->v_stride_seq % 8 || a->v_stride_head % 8 ||
+        a->rope_stride_seq % 4)
+        return fail(FRA_EUNSUPPORTED,
+                    "strides must be multiples of 4 elements (q/k/out/cos/sin) and 8 elements (v)");
+
+    kp.q = (const char *)a->q;
+    kp.k = (const char *)a->k;
+    kp.v = (const char *)a->v;
+    kp.cos = (const char *)a->cos;
+    kp.sin = (const char *)a->sin;
+    kp.out = (char *)a->out;
+    kp.cu = a->cu_seqlens;
+    kp.sq_s = a->q_stride_seq;
+    kp.sq_h = a->q_stride_head;
+    kp.sk_s = a->k_stride_seq;
+    kp.sk_h = a->k_stride_head;
+    kp.sv_s = a->v_stride_seq;
+    kp.sv_h = a->v_stride_head;
+    kp.so_s = a->out_stride_seq;
+    kp.so_h = a->out_stride_head;
+    kp.sr_s = a->rope_stride_seq;
+    kp.total = a->total_seq;
+    kp.num_heads = a->num_heads;
+    kp.num_seqs = a->num_seqs;
+    kp.max_seqlen = a->max_seqlen;
+    kp.scale_log2 = a->softmax_scale * kLog2e;
+
+    const int64_t sh = (int64_t)a->num_seqs * a->num_heads;
+    int64_t grid;
+    if (window) {
+        kp.qblocks = 1;
+        grid = sh;
+        c.kernel = FRA_KERNEL_WINDOW;
+        c.block = 64;
+        c.block_q = 64;
+        c.block_kv = 64;
+        snprintf(c.name, sizeof(c.name), "window_d%d_%s_rope%s", d, dtype_name(a->qkv_dtype),
+                 dtype_name(a->rope_dtype));
+    } else {
+        kp.qblocks = (a->max_seqlen + kLongBQ - 1) / kLongBQ;
+        grid = sh * kp.qblocks;
+        c.kernel = FRA_KERNEL_LONG;
+        c.block = kLongThreads;
+        c.block_q = kLongBQ;
+        c.block_kv = kLongBKV;
+        snprintf(c.name, sizeof(c.name), "long_d%d_%s_rope%s", d, dtype_name(a->qkv_dtype),
+                 dtype_name(a->rope_dtype));
+    }
+    if (grid > 0x7fffffff) return fail(FRA_EUNSUPPORTED, "grid of %lld workgroups is too large", (long long)grid);
+    c.grid = (int)grid;
+    return FRA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fra_fwd_varlen(const fra_fwd_args *args, void *stream) {
+    Choice c;
+    KParams kp;
+    const int rc = plan(args, c, kp);
+    if (rc != FRA_OK) return rc;
+    g_err[0] = 0;
+    if (args->total_seq == 0) return FRA_OK;
+    hipLaunchKernelGGL(c.fn, dim3(c.grid), dim3(c.block), 0, (hipStream_t)stream, kp);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(FRA_EHIP, "launch of %s failed: %s", c.name, hipGetErrorString(e));
+    return FRA_OK;
+}
+
+int fra_query_plan(const fra_fwd_args *args, fra_plan *out) {
+    if (!out) return fail(FRA_EINVAL, "plan is NULL");
+    Choice c;
+    KParams kp;
+    const int rc = plan(args, c, kp);
+    if (rc != FRA_OK) return rc;
+    out->kernel = c.kernel;
+    out->grid = c.grid;
+    out->block = c.block;
+    out->block_q = c.block_q;
+    out->block_kv = c.block_kv;
+    out->lds_bytes = c.lds;
+    memcpy(out->name, c.name, sizeof(out->name));
+    g_err[0] = 0;
+    return FRA_OK;
+}
+
+int fra_supports_head_dim(int32_t head_dim) {
+    Choice c;
+    return pick_kernel(head_dim, true, false, FRA_DTYPE_BF16, FRA_DTYPE_F32, c) ? 1 : 0;
+}
+
+const char *fra_last_error(void) { return g_err; }
+
+const char *fra_version(void) { return "fra 0.1.0 (gfx950)"; }
+
+int32_t fra_abi_version(void) { return FRA_ABI_VERSION; }
+
+int32_t fra_sizeof_args(void) { return (int32_t)sizeof(fra_fwd_args); }
+
+int32_t fra_sizeof_plan(void) { return (int32_t)sizeof(fra_plan); }
+
+}  // extern "C"

@@ -1,0 +1,281 @@
+"""Fused 2D-RoPE + varlen attention for vision encoders, on MI355X.
+
+Drop-in for the reference module ``fused_attn.py``:
+
+* ``fused_rope_attention`` -- reference ``fused_attn.py:139-232``; the
+  device work runs in ``libfra.so`` (hand-written gfx950 HIP kernels behind
+  the C ABI of ``include/fra.h``).  Same argument order, layout, dtype rules,
+  validation messages and return value; ``max_seqlen`` and
+  ``softmax_scale`` are optional extras after ``cu_seqlens``.
+* ``compute_rope_2d`` -- reference ``fused_attn.py:33-136`` (with its LRU
+  cache, ``:18-30``): the cos/sin tables the op consumes.
+* ``next_pow2`` -- reference ``fused_attn.py:13-15``.
+"""
+from collections import OrderedDict
+
+import torch
+
+from . import _lib
+
+__all__ = ["fused_rope_attention", "compute_rope_2d", "next_pow2", "plan"]
+
+
+def next_pow2(n: int) -> int:
+    """Smallest power of 2 >= n (1 for n <= 0), as reference fused_attn.py:13-15."""
+    n = int(n)
+    if n <= 1:
+        return 1
+    return 1 << (n - 1).bit_length()
+
+
+# ---------------------------------------------------------------------------
+# RoPE tables (reference fused_attn.py:18-136)
+# ---------------------------------------------------------------------------
+
+_rope_cache: "OrderedDict[tuple, tuple]" = OrderedDict()
+_ROPE_CACHE_MAX = 32
+
+
+def _device_key(device: torch.device) -> tuple:
+    if device.type == "cuda":
+        return ("cuda", device.index if device.index is not None else torch.cuda.current_device())
+    return (device.type, device.index)
+
+
+def _merge_order(h: int, w: int, merge: int, device) -> tuple:
+    """(h, w) patch coordinates of an h x w grid listed block-major over
+    merge x merge blocks: block row, block column, then the patches of the
+    block row-major (reference fused_attn.py:86-94)."""
+    if h % merge or w % merge:
+        raise RuntimeError(f"grid h={h}, w={w} is not divisible by spatial_merge_size={merge}")
+    mu = merge * merge
+    n = torch.arange(h * w, device=device, dtype=torch.int64)
+    blk, inner = n // mu, n % mu
+    bw_count = w // merge
+    hp = (blk // bw_count) * merge + inner // merge
+    wp = (blk % bw_count) * merge + inner % merge
+    return hp, wp
+
+
+def compute_rope_2d(grid_thw, head_dim: int, spatial_merge_size: int, theta: float, device, dtype,
+                    window_idx: "torch.Tensor | None" = None):
+    """2D vision RoPE tables ``(cos, sin)``, each ``[total_seq, head_dim // 2]``.
+
+    For every image ``(t, h, w)``: patch coordinates in spatial-merge block
+    order, repeated ``t`` times; ``inv_freq = 1/theta**(arange(0, D/2, 2)/(D/2))``;
+    ``emb = [h * inv_freq || w * inv_freq]``; ``cos(emb)``, ``sin(emb)`` cast
+    to ``dtype``.  ``window_idx`` (a permutation of merge units, from
+    ``get_window_index``) reorders the rows into window order.  Results are
+    cached (32 entries, LRU) per (grids, head_dim, merge, theta, device,
+    dtype), as in reference fused_attn.py:71-122.
+    """
+    assert head_dim > 0 and head_dim % 4 == 0, f"head_dim must be divisible by 4, got {head_dim}"
+    rd = head_dim // 2
+    merge = int(spatial_merge_size)
+    device = torch.device(device)
+    if isinstance(grid_thw, torch.Tensor):
+        thw = [tuple(int(x) for x in row) for row in grid_thw.detach().cpu().tolist()]
+    else:
+        thw = [(int(t), int(h), int(w)) for t, h, w in grid_thw]
+
+    key = (tuple(thw), int(head_dim), merge, float(theta), *_device_key(device), dtype)
+    hit = _rope_cache.get(key)
+    if hit is not None:
+        _rope_cache.move_to_end(key)
+        cos, sin = hit
+    else:
+        inv = 1.0 / (theta ** (torch.arange(0, rd, 2, device=device, dtype=torch.float32) / rd))
+        hs, ws = [], []
+        for t, h, w in thw:
+            hp, wp = _merge_order(h, w, merge, device)
+            hs.append(hp.repeat(t))
+            ws.append(wp.repeat(t))
+        hpos = torch.cat(hs).to(torch.float32)
+        wpos = torch.cat(ws).to(torch.float32)
+        emb = torch.cat([torch.outer(hpos, inv), torch.outer(wpos, inv)], dim=1)
+        cos = emb.cos().to(dtype).contiguous()
+        sin = emb.sin().to(dtype).contiguous()
+        _rope_cache[key] = (cos, sin)
+        while len(_rope_cache) > _ROPE_CACHE_MAX:
+            _rope_cache.popitem(last=False)
+
+    if window_idx is not None:
+        mu = merge * merge
+        widx = window_idx.to(device=device, dtype=torch.long)
+        cos = cos.view(-1, mu, rd).index_select(0, widx).reshape(-1, rd)
+        sin = sin.view(-1, mu, rd).index_select(0, widx).reshape(-1, rd)
+    return cos.contiguous(), sin.contiguous()
+
+
+# ---------------------------------------------------------------------------
+# The op (reference fused_attn.py:139-232)
+# ---------------------------------------------------------------------------
+
+_QKV_CODE = {torch.bfloat16: _lib.FRA_DTYPE_BF16, torch.float16: _lib.FRA_DTYPE_F16}
+_ROPE_CODE = {torch.bfloat16: _lib.FRA_DTYPE_BF16, torch.float16: _lib.FRA_DTYPE_F16,
+              torch.float32: _lib.FRA_DTYPE_F32}
+
+
+def _fits(t: torch.Tensor, ptr_align: int, stride_mult: int) -> bool:
+    """True if the kernels can read ``t`` in place: unit stride on the last
+    dim, base aligned to ``ptr_align`` bytes, outer strides multiples of
+    ``stride_mult`` elements."""
+    if t.stride(-1) != 1 and t.shape[-1] > 1:
+        return False
+    if t.data_ptr() % ptr_align:
+        return False
+    return all(s % stride_mult == 0 for s in t.stride()[:-1])
+
+
+def _kernel_layout(t: torch.Tensor, ptr_align: int, stride_mult: int) -> torch.Tensor:
+    return t if _fits(t, ptr_align, stride_mult) else t.contiguous()
+
+
+def _build_args(q, k, v, cos, sin, out, cu, max_seqlen: int, scale: float) -> "_lib.FwdArgs":
+    a = _lib.FwdArgs()
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.cos, a.sin, a.out = cos.data_ptr(), sin.data_ptr(), out.data_ptr()
+    a.cu_seqlens = cu.data_ptr()
+    a.q_stride_seq, a.q_stride_head = q.stride(0), q.stride(1)
+    a.k_stride_seq, a.k_stride_head = k.stride(0), k.stride(1)
+    a.v_stride_seq, a.v_stride_head = v.stride(0), v.stride(1)
+    a.out_stride_seq, a.out_stride_head = out.stride(0), out.stride(1)
+    a.rope_stride_seq = cos.stride(0)
+    a.total_seq, a.num_heads, a.head_dim = q.shape
+    a.num_seqs = cu.numel() - 1
+    a.max_seqlen = int(max_seqlen)
+    a.rope_width = cos.shape[1]
+    a.qkv_dtype = _QKV_CODE[q.dtype]
+    a.rope_dtype = _ROPE_CODE[cos.dtype]
+    a.softmax_scale = float(scale)
+    a.flags = 0
+    return a
+
+
+def _validate(q, k, v, cos, sin, cu_seqlens, out) -> None:
+    """The reference's checks and messages (fused_attn.py:159-185, 195-201),
+    with cos/sin also accepted at width head_dim (HF cat(emb, emb) layout)."""
+    if q.device.type != "cuda":
+        raise ValueError(f"q must be on CUDA, got device={q.device}")
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError(f"q/k/v must have same shape, got q={tuple(q.shape)} k={tuple(k.shape)} v={tuple(v.shape)}")
+    if q.ndim != 3:
+        raise ValueError(f"q/k/v must be [total_seq, num_heads, head_dim], got q.ndim={q.ndim}")
+    total_seq, num_heads, head_dim = (int(q.shape[0]), int(q.shape[1]), int(q.shape[2]))
+    if head_dim <= 0 or head_dim % 2 != 0:
+        raise ValueError(f"head_dim must be positive and even, got {head_dim}")
+    widths = ((total_seq, head_dim // 2), (total_seq, head_dim))
+    if tuple(cos.shape) not in widths or tuple(sin.shape) != tuple(cos.shape):
+        raise ValueError(
+            f"cos/sin must be [total_seq, head_dim//2]={total_seq, head_dim // 2}, "
+            f"got cos={tuple(cos.shape)} sin={tuple(sin.shape)}")
+    if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2:
+        raise ValueError(f"cu_seqlens must be 1D with length >= 2, got {tuple(cu_seqlens.shape)}")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"q dtype must be float16 or bfloat16, got {q.dtype}")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"q/k/v must share dtype, got q={q.dtype} k={k.dtype} v={v.dtype}")
+    if cos.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError(f"cos dtype must be float16, bfloat16 or float32, got {cos.dtype}")
+    if sin.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError(f"sin dtype must be float16, bfloat16 or float32, got {sin.dtype}")
+    if out is not None:
+        if out.shape != q.shape:
+            raise ValueError(f"out must have shape {tuple(q.shape)}, got {tuple(out.shape)}")
+        if out.dtype != q.dtype or out.device != q.device:
+            raise ValueError(f"out must match q dtype/device, got out={out.dtype}/{out.device} q={q.dtype}/{q.device}")
+    for name, t in (("k", k), ("v", v), ("cos", cos), ("sin", sin)):
+        if t.device != q.device:
+            raise ValueError(f"{name} must be on {q.device}, got {t.device}")
+
+
+def _prepare(q, k, v, cos, sin, cu_seqlens):
+    """Kernel-readable views: strided q/k/v are used in place when their
+    last dim is contiguous and aligned (packed qkv views from a fused qkv
+    projection qualify); anything else is copied, as the reference copies
+    non-contiguous inputs (fused_attn.py:187-193)."""
+    q = _kernel_layout(q, 8, 4)
+    k = _kernel_layout(k, 8, 4)
+    v = _kernel_layout(v, 16, 8)
+    if cos.dtype != sin.dtype:
+        # One table dtype per call: widening bf16/f16 to fp32 is exact.
+        cos, sin = cos.float(), sin.float()
+    ra = 16 if cos.dtype == torch.float32 else 8
+    if not (_fits(cos, ra, 4) and _fits(sin, ra, 4) and cos.stride(0) == sin.stride(0)):
+        cos, sin = cos.contiguous(), sin.contiguous()
+    cu = cu_seqlens
+    if cu.dtype != torch.int32 or cu.device != q.device or not cu.is_contiguous():
+        cu = cu.to(device=q.device, dtype=torch.int32).contiguous()
+    return q, k, v, cos, sin, cu
+
+
+def plan(q, k, v, cos, sin, cu_seqlens, max_seqlen: int, softmax_scale=None) -> dict:
+    """Which kernel ``fused_rope_attention`` launches for these inputs
+    (no launch): ``{"kernel", "name", "grid", "block", "block_q",
+    "block_kv", "lds_bytes"}``."""
+    q2, k2, v2, cos2, sin2, cu = _prepare(q, k, v, cos, sin, cu_seqlens)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    scale = q.shape[2] ** -0.5 if softmax_scale is None else softmax_scale
+    a = _build_args(q2, k2, v2, cos2, sin2, out, cu, max_seqlen, scale)
+    lib = _lib.load()
+    pl = _lib.Plan()
+    _lib.check(lib.fra_query_plan(a, pl))
+    return {"kernel": {_lib.FRA_KERNEL_WINDOW: "window", _lib.FRA_KERNEL_LONG: "long"}.get(pl.kernel, "none"),
+            "name": pl.name.decode(), "grid": pl.grid, "block": pl.block, "block_q": pl.block_q,
+            "block_kv": pl.block_kv, "lds_bytes": pl.lds_bytes}
+
+
+def fused_rope_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    max_seqlen: "int | None" = None,
+    softmax_scale: "float | None" = None,
+    *,
+    out: "torch.Tensor | None" = None,
+) -> torch.Tensor:
+    """Fused split-half RoPE on Q and K + non-causal attention over packed
+    segments (reference fused_attn.py:139-232).
+
+    Shapes:
+      - q, k, v: ``[total_seq, num_heads, head_dim]``, float16 or bfloat16;
+        any outer strides with a contiguous last dim are read in place.
+      - cos, sin: ``[total_seq, head_dim // 2]`` (reference layout) or
+        ``[total_seq, head_dim]`` (HF ``cat(emb, emb)`` layout); float32,
+        bfloat16 or float16.
+      - cu_seqlens: ``[num_segments + 1]`` cumulative token offsets (any int
+        dtype; converted to int32 on q's device).
+      - max_seqlen: longest segment.  ``None`` computes it on the device and
+        synchronises once (as the reference always does); passing it keeps
+        the call free of host synchronisation (graph-capturable).
+      - softmax_scale: defaults to ``head_dim ** -0.5``.
+      - out: optional ``[total_seq, num_heads, head_dim]`` result buffer.
+
+    Rows outside every segment are left unwritten, as in the reference.
+    Returns ``out``.
+    """
+    _validate(q, k, v, cos, sin, cu_seqlens, out)
+    qk, kk, vk, cosk, sink, cu = _prepare(q, k, v, cos, sin, cu_seqlens)
+
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dst = out if _fits(out, 8, 4) else torch.empty(q.shape, dtype=q.dtype, device=q.device)
+
+    if max_seqlen is None:
+        max_seqlen = int((cu[1:] - cu[:-1]).max().item())
+    max_seqlen = int(max_seqlen)
+    if max_seqlen <= 0 or q.shape[0] == 0:
+        return out.zero_()
+    scale = q.shape[2] ** -0.5 if softmax_scale is None else float(softmax_scale)
+
+    lib = _lib.load()
+    args = _build_args(qk, kk, vk, cosk, sink, dst, cu, max_seqlen, scale)
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        _lib.check(lib.fra_fwd_varlen(args, stream))
+    if dst is not out:
+        out.copy_(dst)
+    return out

@@ -1,0 +1,145 @@
+/*
+ * fra.h -- C ABI of the MI355X (gfx950) fused RoPE + varlen attention library
+ * (libfra.so).
+ *
+ * The library replaces the device side of the reference's one hot path:
+ *
+ *   reference fused_attn.py:218-231  the launch of fused_attn_kernel[grid](...)
+ *   reference fused_attn.py:235-423  the Triton kernel itself
+ *
+ * The Python entry point fused_rope_attention() of the reference
+ * (fused_attn.py:139-232) is mirrored one level up, in
+ * fused_rope_attn_amd/fused_attn.py, and calls fra_fwd_varlen() below.
+ *
+ * Conventions
+ *   - Plain C: POD arguments, device pointers, element strides, int status.
+ *   - No C++ exception crosses this boundary; every entry point returns a
+ *     status code and leaves a message for fra_last_error().
+ *   - All work is enqueued on the caller's HIP stream; nothing is
+ *     synchronised, nothing is allocated, no global state is mutated, so the
+ *     calls are reentrant and capturable into a HIP graph.
+ *   - Tensors are [total_seq, num_heads, head_dim] with unit stride on
+ *     head_dim; the two outer strides are free (packed qkv views work).
+ */
+#ifndef FRA_H
+#define FRA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FRA_ABI_VERSION 1
+
+/* Element types. */
+enum fra_dtype {
+    FRA_DTYPE_BF16 = 0,
+    FRA_DTYPE_F16 = 1,
+    FRA_DTYPE_F32 = 2
+};
+
+/* Status codes (0 = success, negative = failure). */
+enum fra_status {
+    FRA_OK = 0,
+    FRA_EINVAL = -1,        /* invalid argument: null pointer, bad shape, enum or stride */
+    FRA_EUNSUPPORTED = -2,  /* valid request this build does not implement (head_dim, alignment) */
+    FRA_EHIP = -3           /* the HIP runtime reported an error at launch */
+};
+
+/* Kernel families chosen by the dispatcher. */
+enum fra_kernel {
+    FRA_KERNEL_NONE = 0,
+    FRA_KERNEL_WINDOW = 1,  /* every segment <= 64 tokens: one (segment, head) per wavefront */
+    FRA_KERNEL_LONG = 2     /* split-Q flash tiling over K/V blocks staged in LDS */
+};
+
+/*
+ * Arguments of one forward call.  Mirrors the argument list of the
+ * reference launch (fused_attn.py:219-231): the six tensors, cu_seqlens,
+ * the strides, NUM_WINDOWS / NUM_HEADS / MAX_SEQLEN and HEAD_DIM, plus the
+ * softmax scale that the reference hard-codes as 1/sqrt(head_dim)
+ * (fused_attn.py:353-355) and the cos/sin width and dtypes it infers from
+ * the tensors.
+ */
+typedef struct fra_fwd_args {
+    const void *q;              /* [total_seq, num_heads, head_dim], qkv_dtype */
+    const void *k;
+    const void *v;
+    const void *cos;            /* [total_seq, rope_width], rope_dtype */
+    const void *sin;            /* same shape, dtype and strides as cos */
+    void *out;                  /* [total_seq, num_heads, head_dim], qkv_dtype */
+    const int32_t *cu_seqlens;  /* device, [num_seqs + 1], cumulative token offsets */
+    int64_t q_stride_seq, q_stride_head;      /* in elements; head_dim stride is 1 */
+    int64_t k_stride_seq, k_stride_head;
+    int64_t v_stride_seq, v_stride_head;
+    int64_t out_stride_seq, out_stride_head;
+    int64_t rope_stride_seq;    /* in elements, shared by cos and sin */
+    int32_t total_seq;          /* rows of q/k/v/out/cos/sin; segments are clamped to it */
+    int32_t num_heads;
+    int32_t head_dim;
+    int32_t num_seqs;           /* number of segments = len(cu_seqlens) - 1 */
+    int32_t max_seqlen;         /* >= 1 and >= every segment length */
+    int32_t rope_width;         /* head_dim/2 (reference layout) or head_dim (HF cat(emb, emb)) */
+    int32_t qkv_dtype;          /* FRA_DTYPE_BF16 or FRA_DTYPE_F16 */
+    int32_t rope_dtype;         /* FRA_DTYPE_F32, FRA_DTYPE_BF16 or FRA_DTYPE_F16 */
+    float softmax_scale;        /* > 0; the reference uses 1/sqrt(head_dim) */
+    int32_t flags;              /* reserved, must be 0 */
+} fra_fwd_args;
+
+/* What fra_fwd_varlen() would launch for a set of arguments. */
+typedef struct fra_plan {
+    int32_t kernel;             /* enum fra_kernel */
+    int32_t grid;               /* workgroups (1-D grid) */
+    int32_t block;              /* threads per workgroup */
+    int32_t block_q;            /* query rows per workgroup */
+    int32_t block_kv;           /* key/value rows per LDS stage */
+    int32_t lds_bytes;          /* static LDS per workgroup */
+    char name[64];              /* kernel instance name */
+} fra_plan;
+
+/*
+ * Fused split-half RoPE on Q and K + non-causal softmax attention over the
+ * packed segments [cu_seqlens[i], cu_seqlens[i+1]).  Replaces
+ * reference fused_attn.py:218-231 (+ the kernel at :235-423).
+ *
+ * Semantics (as the reference kernel): the rotation is computed in fp32 and
+ * rounded to the input dtype (fused_attn.py:340-345, 385-390); logits are
+ * scaled by softmax_scale*log2(e) and exponentiated with exp2 (:353-355,
+ * :398-405); P is rounded to the value dtype before PV (:413); fp32
+ * accumulation; the output is acc / rowsum rounded to the output dtype
+ * (:417-423).  Empty segments are skipped (:295-296).  Rows outside every
+ * segment are not written (:196).  Segment bounds are clamped to
+ * [0, total_seq], so a malformed cu_seqlens never reads or writes outside
+ * the tensors; a max_seqlen below the true maximum gives unspecified values
+ * in the rows of the longer segments, never an out-of-bounds access.
+ *
+ * `stream` is a hipStream_t (NULL = the null stream).
+ * Returns FRA_OK or a negative enum fra_status.
+ */
+int fra_fwd_varlen(const fra_fwd_args *args, void *stream);
+
+/* Fill *plan with the kernel choice for args without launching anything. */
+int fra_query_plan(const fra_fwd_args *args, fra_plan *plan);
+
+/* 1 if head_dim has a compiled kernel in this build, else 0. */
+int fra_supports_head_dim(int32_t head_dim);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *fra_last_error(void);
+
+/* Library version string. */
+const char *fra_version(void);
+
+/* FRA_ABI_VERSION of the built library. */
+int32_t fra_abi_version(void);
+
+/* sizeof(fra_fwd_args) / sizeof(fra_plan) as compiled, for FFI checks. */
+int32_t fra_sizeof_args(void);
+int32_t fra_sizeof_plan(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FRA_H */

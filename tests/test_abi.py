@@ -1,0 +1,126 @@
+"""The C ABI of libfra.so without a GPU: the library loads, exports every
+symbol include/fra.h declares, its structs match the ctypes mirrors, and the
+dispatcher's validation and kernel choice behave (no kernel is launched:
+every call here fails validation, or has total_seq == 0, or is a plan query)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from fused_rope_attn_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fra.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z0-9_]+\s*\*?\s*(fra_[a-z0-9_]+)\s*\(", text, re.M)))
+
+
+def test_header_declares_what_the_binding_types():
+    syms = header_symbols()
+    assert syms, "no declarations parsed"
+    assert set(syms) == set(_lib.SIGNATURES), (syms, sorted(_lib.SIGNATURES))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in header_symbols():
+        assert hasattr(lib, name), name
+    assert lib.fra_abi_version() == _lib.ABI_VERSION
+    assert lib.fra_sizeof_args() == ctypes.sizeof(_lib.FwdArgs)
+    assert lib.fra_sizeof_plan() == ctypes.sizeof(_lib.Plan)
+    assert b"gfx950" in lib.fra_version()
+
+
+def make_args(**kw):
+    a = _lib.FwdArgs()
+    n, h, d = kw.get("n", 1024), kw.get("h", 16), kw.get("d", 80)
+    base = 1 << 20  # fake, aligned device addresses: nothing is launched
+    a.q, a.k, a.v, a.cos, a.sin, a.out = (base * (i + 1) for i in range(6))
+    a.cu_seqlens = base * 8
+    a.q_stride_seq = a.k_stride_seq = a.v_stride_seq = a.out_stride_seq = h * d
+    a.q_stride_head = a.k_stride_head = a.v_stride_head = a.out_stride_head = d
+    a.rope_stride_seq = d // 2
+    a.total_seq, a.num_heads, a.head_dim = n, h, d
+    a.num_seqs = kw.get("nseg", 16)
+    a.max_seqlen = kw.get("max_seqlen", 64)
+    a.rope_width = d // 2
+    a.qkv_dtype, a.rope_dtype = _lib.FRA_DTYPE_BF16, _lib.FRA_DTYPE_F32
+    a.softmax_scale = d ** -0.5
+    a.flags = 0
+    for key, val in kw.items():
+        if key not in ("n", "h", "d", "nseg"):
+            setattr(a, key, val)
+    return a
+
+
+def plan_of(a):
+    p = _lib.Plan()
+    rc = _lib.load().fra_query_plan(a, p)
+    return rc, p
+
+
+def test_plan_window_and_long():
+    rc, p = plan_of(make_args())
+    assert rc == _lib.FRA_OK
+    assert p.kernel == _lib.FRA_KERNEL_WINDOW and p.grid == 16 * 16 and p.block == 64
+    assert p.name.decode() == "window_d80_bf16_ropef32"
+    rc, p = plan_of(make_args(max_seqlen=9216, num_seqs=1, n=9216))
+    assert rc == _lib.FRA_OK and p.kernel == _lib.FRA_KERNEL_LONG
+    assert p.grid == 16 * ((9216 + p.block_q - 1) // p.block_q)
+    rc, p = plan_of(make_args(d=128, max_seqlen=64))
+    assert rc == _lib.FRA_OK and p.kernel == _lib.FRA_KERNEL_LONG  # window kernel is for D <= 96
+    rc, p = plan_of(make_args(d=72, max_seqlen=64, qkv_dtype=_lib.FRA_DTYPE_F16, rope_dtype=_lib.FRA_DTYPE_BF16))
+    assert rc == _lib.FRA_OK and p.name.decode() == "window_d72_f16_ropebf16"
+
+
+@pytest.mark.parametrize("field,value,code,msg", [
+    ("q", 0, _lib.FRA_EINVAL, "NULL"),
+    ("cu_seqlens", 0, _lib.FRA_EINVAL, "NULL"),
+    ("num_heads", 0, _lib.FRA_EINVAL, "num_heads"),
+    ("head_dim", 81, _lib.FRA_EINVAL, "even"),
+    ("head_dim", 0, _lib.FRA_EINVAL, "even"),
+    ("num_seqs", 0, _lib.FRA_EINVAL, "num_seqs"),
+    ("max_seqlen", 0, _lib.FRA_EINVAL, "max_seqlen"),
+    ("qkv_dtype", _lib.FRA_DTYPE_F32, _lib.FRA_EINVAL, "qkv_dtype"),
+    ("rope_dtype", 7, _lib.FRA_EINVAL, "rope_dtype"),
+    ("rope_width", 33, _lib.FRA_EINVAL, "rope_width"),
+    ("softmax_scale", 0.0, _lib.FRA_EINVAL, "softmax_scale"),
+    ("softmax_scale", float("nan"), _lib.FRA_EINVAL, "softmax_scale"),
+    ("flags", 1, _lib.FRA_EINVAL, "flags"),
+    ("q_stride_seq", -1280, _lib.FRA_EINVAL, "strides"),
+    ("v", (1 << 20) + 8, _lib.FRA_EUNSUPPORTED, "aligned"),
+    ("q", (1 << 20) + 4, _lib.FRA_EUNSUPPORTED, "aligned"),
+    ("v_stride_seq", 1284, _lib.FRA_EUNSUPPORTED, "multiples"),
+    ("q_stride_head", 82, _lib.FRA_EUNSUPPORTED, "multiples"),
+])
+def test_validation_errors(field, value, code, msg):
+    a = make_args(**{field: value})
+    lib = _lib.load()
+    rc, _ = plan_of(a)
+    assert rc == code
+    assert msg in lib.fra_last_error().decode()
+    assert lib.fra_fwd_varlen(a, None) == code  # fails before any launch
+
+
+def test_unsupported_head_dim():
+    lib = _lib.load()
+    for d in (64, 72, 80, 96, 128):
+        assert lib.fra_supports_head_dim(d) == 1
+    for d in (2, 66, 88, 256):
+        assert lib.fra_supports_head_dim(d) == 0
+        a = make_args(d=d)
+        assert lib.fra_fwd_varlen(a, None) == _lib.FRA_EUNSUPPORTED
+        assert "head_dim" in lib.fra_last_error().decode()
+
+
+def test_null_args_and_empty_problem():
+    lib = _lib.load()
+    assert lib.fra_fwd_varlen(None, None) == _lib.FRA_EINVAL
+    assert lib.fra_query_plan(make_args(), None) == _lib.FRA_EINVAL
+    # total_seq == 0 validates and returns without launching
+    assert lib.fra_fwd_varlen(make_args(n=0), None) == _lib.FRA_OK
+    assert lib.fra_last_error() == b""
