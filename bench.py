@@ -9,8 +9,9 @@ the HBM roofline.
 Protocol:
 * inputs are synthetic (q, k, v ~ N(0, 1), seeded) and resident in HBM;
 * ``--warmup`` untimed calls, then ``--steps`` timed calls; before each timed
-  call a 1 GiB buffer is overwritten so that neither the L2s nor the 256 MB
-  Infinity Cache hold the inputs (the cold number is the headline); each call
+  call a 1 GiB buffer is read (a reduction over it), so that neither the L2s
+  nor the 256 MB Infinity Cache hold the inputs and no dirty lines are left
+  for the timed call to write back (the cold number is the headline); each call
   is bracketed by HIP events on the stream the kernel runs on (torch's
   current stream); ``value`` is the median;
 * the warm number is the same call back to back, total time / steps;
@@ -55,6 +56,12 @@ def workload_cost(w, inp):
     return n, lens, nbytes, flops
 
 
+def evict(flush: torch.Tensor) -> None:
+    """Read the whole flush buffer: the caches end up holding its (clean)
+    lines instead of the workload's inputs."""
+    torch.sum(flush, dtype=torch.int32)
+
+
 def measure(inp, steps: int, warmup: int, flush: torch.Tensor) -> dict:
     q, k, v, cos, sin, cu = (inp[x] for x in ("q", "k", "v", "cos", "sin", "cu_seqlens"))
     ms = inp["max_seqlen"]
@@ -73,7 +80,7 @@ def measure(inp, steps: int, warmup: int, flush: torch.Tensor) -> dict:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        flush.fill_(i & 0x7F)
+        evict(flush)
         starts[i].record(stream)
         call()
         ends[i].record(stream)
@@ -150,6 +157,33 @@ def run_workload(name: str, steps: int, warmup: int, flush: torch.Tensor, dev) -
             "warm_achieved": (nbytes if hbm else flops) / (m["warm_us"] * 1e-6) / (1e9 if hbm else 1e12)}, inp
 
 
+def profile_driver(args, flush, dev) -> int:
+    """Kernel launches for rocprofv3: warmup, then ``--profile-calls`` calls of
+    the workload each after a cache flush, then one copy of known size whose
+    FETCH_SIZE / WRITE_SIZE calibrate the counters (it reads and writes
+    exactly ``--copy-mib`` MiB)."""
+    w = WORKLOADS[args.workload]
+    inp = make_inputs(w, seed=1234 + list(WORKLOADS).index(args.workload), device=dev)
+    q, k, v, cos, sin, cu = (inp[x] for x in ("q", "k", "v", "cos", "sin", "cu_seqlens"))
+    out = torch.empty_like(q)
+    for _ in range(3):
+        fused_rope_attention(q, k, v, cos, sin, cu, inp["max_seqlen"], out=out)
+    for i in range(args.profile_calls):
+        evict(flush)
+        fused_rope_attention(q, k, v, cos, sin, cu, inp["max_seqlen"], out=out)
+    torch.cuda.synchronize()
+    n = args.copy_mib << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    flush.fill_(1)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    n_tok, lens, nbytes, flops = workload_cost(w, inp)
+    print(json.dumps({"profile_driver": args.workload, "calls": args.profile_calls, "bytes": nbytes,
+                      "flops": flops, "copy_bytes_each_way": n}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -159,6 +193,10 @@ def main() -> int:
     ap.add_argument("--report", default=None, help="measure every workload and write them to this JSON file")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-calls", type=int, default=0,
+                    help="profiling driver: run this many cold calls of --workload, then a plain "
+                         "device copy of --copy-mib MiB (HBM counter calibration), and exit")
+    ap.add_argument("--copy-mib", type=int, default=256)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -169,7 +207,9 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     dev = torch.device("cuda:0")
-    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
+    flush = torch.ones(FLUSH_BYTES, dtype=torch.uint8, device=dev)
+    if args.profile_calls:
+        return profile_driver(args, flush, dev)
 
     torch.cuda.synchronize()
     res, inp = run_workload(args.workload, args.steps, args.warmup, flush, dev)
@@ -190,7 +230,7 @@ def main() -> int:
         "config": {"workload": f"{args.workload}: {w.note}", "tokens": res["tokens"], "segments": res["segments"],
                    "max_seqlen": res["max_seqlen"], "heads": w.heads, "head_dim": w.head_dim,
                    "qkv": "bf16 [N, H, D]", "rope": f"fp32 [N, {w.head_dim // 2}]",
-                   "cache": "cold: 1 GiB overwritten before each timed call", "parallelism": "single GPU"},
+                   "cache": "cold: 1 GiB read before each timed call", "parallelism": "single GPU"},
         "roofline": dict(res["roofline"], traffic=None),
         "kernel": res["kernel"],
         "cold_p10_us": round(res["cold_p10_us"], 3),

@@ -31,6 +31,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "fra.h"
 
 namespace {
@@ -132,6 +134,13 @@ __device__ __forceinline__ float xchg32(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, x)));
 }
 
+// An opaque copy of v: index arithmetic derived from it is recomputed in each
+// phase instead of being kept live (in registers) across the whole kernel.
+__device__ __forceinline__ int fresh(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 __device__ __forceinline__ u32 perm(u32 hi_src, u32 lo_src, u32 sel) {
     return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
@@ -186,93 +195,275 @@ __device__ __forceinline__ void load_rotate_quad(const char *xrow, const char *c
 
 // ---- window kernel ------------------------------------------------------------
 //
-// One wavefront per (segment, head), segment length L <= 64.  Lane (r, g)
-// (r = lane & 31, g = lane >> 5) holds the operands of tokens r and r + 32:
-// K_rot rows as the A operand of S^T and Q_rot rows as its B operand.
+// One workgroup of 4 wavefronts per (segment, group of 4 heads); segment
+// length L <= 64.  All HBM traffic is coalesced: consecutive lanes move
+// consecutive 16-byte chunks of the group's slab -- 4 heads x D elements,
+// contiguous in a [tokens, heads, head_dim] tensor -- and LDS turns the slab
+// into MFMA operands (and the output back into slab rows).
+//
+//   1. every global load is issued up front: cos/sin rows, Q, K, V slabs;
+//   2. cos/sin -> LDS as fp32 rows; the Q slab -> LDS (whole, or one
+//      32-token half at a time when the LDS budget asks for it), where
+//      wavefront w rotates the quads of head 4*hg + w it feeds (fp32, rounded
+//      to the storage dtype);
+//   3. the same for K;
+//   4. V -> LDS transposed (V^T per head, kv pairs packed in dwords);
+//   5. per 32-query tile: S^T = K_rot Q_rot^T, softmax, O^T = V^T P^T; the
+//      normalised output stays in registers as packed bf16/fp16;
+//   6. the output rows go through LDS (over V^T) and leave as slab rows.
+//
+// Lane (r, g) (r = lane & 31, g = lane >> 5) of a wavefront holds the
+// operands of tokens r and r + 32: K_rot rows as the A operand of S^T and
+// Q_rot rows as its B operand; MFMA step t, k-slot group g carries
+// {x0r[4i..4i+3], x1r[4i..4i+3]} of quad i = g*S + t (the contraction order is
+// free as long as Q and K share it).
+
+constexpr int kWinHeads = 4;     // heads (wavefronts) per workgroup
+constexpr int kWinWaves = 2;     // wavefronts per SIMD the register budget is sized for
+constexpr int kWinThreads = 64 * kWinHeads;
+
+template <int D, bool FULL> struct WinLds {
+    static constexpr int W = FULL ? D : D / 2;         // table width
+    static constexpr int CS = 2 * W + 4;               // fp32 per [cos | sin] row, +4 pad (conflict-free b128 reads)
+    static constexpr int SLAB = kWinHeads * D * 2;     // bytes of one token's slab
+    static constexpr int PITCH = SLAB + 16;            // LDS row pitch of a staged slab (one pad chunk)
+    static constexpr int VTS = 36;                     // dwords per V^T row: 32 kv pairs + 4 pad
+    static constexpr int kTableBytes = 64 * CS * 4;
+    static constexpr int kStageRows = kWinWaves == 2 ? 64 : 32;  // slab rows staged at once
+    static constexpr int kHalfBytes = kStageRows * PITCH;
+    static constexpr int kRotBytes = kTableBytes + kHalfBytes;
+    static constexpr int kVtBytes = kWinHeads * D * VTS * 4;
+    static constexpr int kOutBytes = 64 * PITCH;
+    static constexpr int kMax2 = kVtBytes > kOutBytes ? kVtBytes : kOutBytes;
+    static constexpr int kMain = kRotBytes > kMax2 ? kRotBytes : kMax2;
+    static constexpr int kBytes = kMain + 16;          // + a 16-byte trash slot
+};
 
 template <int D, class E, int RD, bool FULL>
-__global__ __launch_bounds__(64, 3) void window_kernel(const KParams p) {
-    constexpr int HALF = D / 2;
-    constexpr int NQ = D / 8;           // quads per half
-    constexpr int S = (NQ + 1) / 2;     // 16-deep k-steps of QK^T
-    constexpr int NCH = D / 8;          // 16-byte chunks per V row
-    constexpr int CH0 = (NCH + 1) / 2;  // chunks staged by lane group 0
-    constexpr int NDT = (D + 31) / 32;  // 32-row tiles of O^T
-    constexpr int VTS = 34;             // dwords per V^T row: 32 kv pairs + 2 pad
-    constexpr int VROWS = 16 * CH0;     // staged rows incl. the scratch rows of a missing odd chunk
-    __shared__ u32 vt[VROWS * VTS];
+__global__ __launch_bounds__(kWinThreads, kWinWaves) void window_kernel(const KParams p) {
+    using LDS = WinLds<D, FULL>;
+    constexpr int NQ = D / 8;                 // quads per half
+    constexpr int S = (NQ + 1) / 2;           // 16-deep k-steps of QK^T
+    constexpr int NDT = (D + 31) / 32;        // 32-row tiles of O^T
+    constexpr int VTS = LDS::VTS;
+    constexpr int W = LDS::W;
+    constexpr int CS = LDS::CS;
+    constexpr int PITCH = LDS::PITCH;
+    constexpr int HCH = D / 8;                // 16-byte chunks per head row
+    constexpr int NCH = kWinHeads * HCH;      // chunks per slab row
+    constexpr int RB = Rope<RD>::kBytes;
+    constexpr int TQ = W / 4;                 // table quads per row
+    constexpr int TITEMS = 64 * TQ * 2;       // (token, quad, table)
+    constexpr int TPER = (TITEMS + kWinThreads - 1) / kWinThreads;
+    constexpr int SITEMS = 64 * NCH;          // (token, chunk) of a Q/K slab or the output
+    constexpr int SPER = (SITEMS + kWinThreads - 1) / kWinThreads;
+    constexpr int VITEMS = 32 * NCH;          // (token pair, chunk) of the V slab
+    constexpr int VPER = (VITEMS + kWinThreads - 1) / kWinThreads;
+    constexpr int OQ = NDT * 4;               // output quads per lane and query tile
+    // V^T row rho (= head*D + d) stores kv pair j at dword column
+    // j ^ vswz(rho): with the 36-dword pitch this makes both the staging
+    // writes and the operand reads (b64, pairs of columns) 2-way at most
+    // across the 64 banks.  The xor value is even, so column pairs stay
+    // adjacent and 8-byte aligned.
+    auto vswz = [](int rho) { return 2 * ((rho >> 4) & 15); };
+    __shared__ __attribute__((aligned(16))) char lds[LDS::kBytes];
+    float *tab = (float *)lds;                                  // [64][CS] fp32 tables
+    char *half = lds + LDS::kTableBytes;                        // [32][PITCH]: half a Q or K slab
+    u32 *vt_all = (u32 *)lds;                                   // [4][D][VTS] V^T, after the rotations
+    char *oslab = lds;                                          // [64][PITCH] output rows, after PV
+    char *trash = lds + LDS::kMain;                             // sink of out-of-range staging items
 
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int r = lane & 31, g = lane >> 5;
+    const int ngroups = (p.num_heads + kWinHeads - 1) / kWinHeads;
     const int u = xcd_remap(blockIdx.x, gridDim.x);
-    const int seg = u / p.num_heads, head = u - seg * p.num_heads;
+    const int seg = u / ngroups, hg = u - seg * ngroups;
+    const int h0 = hg * kWinHeads;
+    const int nh = min(kWinHeads, p.num_heads - h0);            // heads in this group
+    const bool active = w < nh;  // wavefronts past the last head still take part in barriers
     int s0 = p.cu[seg], s1 = p.cu[seg + 1];
     s0 = min(max(s0, 0), p.total);
     s1 = min(max(s1, 0), p.total);
     const int L = min(s1 - s0, 64);
-    if (L <= 0) return;
+    if (L <= 0) return;  // uniform across the workgroup
 
-    // V^T staging: lane (r, g) packs kv rows 2r and 2r+1 for chunks
-    // [g*CH0, g*CH0 + CH0); vt[d][r] holds {V[2r][d], V[2r+1][d]}.  Rows
-    // past the segment are read at its first row and zeroed; a chunk index
-    // past the row (odd NCH) reads chunk 0 and lands in scratch rows >= D.
-    {
-        const int ra = 2 * r, rb = 2 * r + 1;
-        const bool va = ra < L, vb = rb < L;
-        const int64_t hoff = (int64_t)head * p.sv_h;
-        const char *pa = p.v + ((int64_t)(s0 + (va ? ra : 0)) * p.sv_s + hoff) * 2;
-        const char *pb = p.v + ((int64_t)(s0 + (vb ? rb : 0)) * p.sv_s + hoff) * 2;
-        u32x4 A[CH0], B[CH0];
+    // Wave-uniform 64-bit bases plus 32-bit per-lane byte offsets: the host
+    // guarantees 64 rows of every tensor span < 2 GiB.
+    const char *qb = p.q + ((int64_t)s0 * p.sq_s + (int64_t)h0 * p.sq_h) * 2;
+    const char *kb = p.k + ((int64_t)s0 * p.sk_s + (int64_t)h0 * p.sk_h) * 2;
+    const char *vb = p.v + ((int64_t)s0 * p.sv_s + (int64_t)h0 * p.sv_h) * 2;
+    const char *cb = p.cos + (int64_t)s0 * p.sr_s * RB;
+    const char *sb = p.sin + (int64_t)s0 * p.sr_s * RB;
+    char *ob = p.out + ((int64_t)s0 * p.so_s + (int64_t)h0 * p.so_h) * 2;
+    const uint32_t qrs = (uint32_t)p.sq_s * 2, krs = (uint32_t)p.sk_s * 2, vrs = (uint32_t)p.sv_s * 2;
+    const uint32_t qhs = (uint32_t)p.sq_h * 2, khs = (uint32_t)p.sk_h * 2, vhs = (uint32_t)p.sv_h * 2;
+    const uint32_t ors = (uint32_t)p.so_s * 2, ohs = (uint32_t)p.so_h * 2;
+    const uint32_t trs = (uint32_t)p.sr_s * RB;
+
+    // ---- 1. every global load, back to back: tables, Q, K and V slabs ----------
+    // Rows past the segment and chunks of heads past the last one read the
+    // segment's first row / the group's first head; their values are never used.
+    f32x4 tv[TPER];
+    int t1 = fresh(tid);
 #pragma unroll
-        for (int cc = 0; cc < CH0; ++cc) {
-            const int c = g * CH0 + cc;
-            const int cl = c < NCH ? c : 0;
-            A[cc] = *(const u32x4 *)(pa + 16 * cl);
-            B[cc] = *(const u32x4 *)(pb + 16 * cl);
-        }
-#pragma unroll
-        for (int cc = 0; cc < CH0; ++cc) {
-            const int c = g * CH0 + cc;
-            if (!va) A[cc] = u32x4{0u, 0u, 0u, 0u};
-            if (!vb) B[cc] = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                vt[(8 * c + 2 * j) * VTS + r] = perm(B[cc][j], A[cc][j], kSelLo);
-                vt[(8 * c + 2 * j + 1) * VTS + r] = perm(B[cc][j], A[cc][j], kSelHi);
-            }
-        }
+    for (int k = 0; k < TPER; ++k) {
+        const int it = min(t1 + k * kWinThreads, TITEMS - 1);
+        const int tok = it / (2 * TQ), rem = it - tok * 2 * TQ;
+        const int tbl = rem / TQ, qd = rem - tbl * TQ;
+        const uint32_t off = (uint32_t)(tok < L ? tok : 0) * trs + (uint32_t)(4 * qd * RB);
+        tv[k] = Rope<RD>::quad((tbl ? sb : cb) + off);
     }
-
-    // Q_rot / K_rot operands in registers.
-    u32x4 qop[2][S], kop[2][S];
+    u32x4 qs[SPER], ks[SPER];
+    t1 = fresh(tid);
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        const int tok = r + 32 * tt;
-        const bool valid = tok < L;
-        const int64_t row = s0 + (valid ? tok : 0);
-        const char *qrow = p.q + (row * p.sq_s + (int64_t)head * p.sq_h) * 2;
-        const char *krow = p.k + (row * p.sk_s + (int64_t)head * p.sk_h) * 2;
-        const char *crow = p.cos + row * p.sr_s * Rope<RD>::kBytes;
-        const char *srow = p.sin + row * p.sr_s * Rope<RD>::kBytes;
+    for (int k = 0; k < SPER; ++k) {
+        const int it = min(t1 + k * kWinThreads, SITEMS - 1);
+        const int tok = it / NCH, wc = it - tok * NCH;
+        const int hh = wc / HCH, c = wc - hh * HCH;
+        const uint32_t row = tok < L ? tok : 0, hd = hh < nh ? hh : 0;
+        qs[k] = *(const u32x4 *)(qb + (row * qrs + hd * qhs + 16 * c));
+        ks[k] = *(const u32x4 *)(kb + (row * krs + hd * khs + 16 * c));
+    }
+    // V rows 2j, 2j+1 of the slab.
+    u32x4 va[VPER], vv[VPER];
+    t1 = fresh(tid);
+#pragma unroll
+    for (int k = 0; k < VPER; ++k) {
+        const int it = min(t1 + k * kWinThreads, VITEMS - 1);
+        const int j = it / NCH, wc = it - j * NCH;
+        const int hh = wc / HCH, c = wc - hh * HCH;
+        const uint32_t ra = 2 * j < L ? 2 * j : 0, rb = 2 * j + 1 < L ? 2 * j + 1 : 0;
+        const uint32_t hd = hh < nh ? hh : 0;
+        va[k] = *(const u32x4 *)(vb + (ra * vrs + hd * vhs + 16 * c));
+        vv[k] = *(const u32x4 *)(vb + (rb * vrs + hd * vhs + 16 * c));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 2. tables to LDS; Q staged and rotated ---------------------------------
+    // Staging writes are branch-free (a branch here would make the compiler
+    // wait for every outstanding load): items out of range go to the trash slot.
+    t1 = fresh(tid);
+#pragma unroll
+    for (int k = 0; k < TPER; ++k) {
+        const int it = t1 + k * kWinThreads;
+        const bool in = TITEMS % kWinThreads == 0 || it < TITEMS;
+        const int itc = in ? it : 0;
+        const int tok = itc / (2 * TQ), rem = itc - tok * 2 * TQ;
+        const int tbl = rem / TQ, qd = rem - tbl * TQ;
+        *(f32x4 *)(in ? (char *)(tab + tok * CS + tbl * W + 4 * qd) : trash) = tv[k];
+    }
+    // Writes the items of tokens [R*hf, R*hf + R) of a slab into `half`
+    // (R = kStageRows: all 64 rows at once when LDS allows, else 32).
+    constexpr int R = LDS::kStageRows;
+    auto stage_half = [&](const u32x4 (&x)[SPER], int hf) {
+        const int ts = fresh(tid);
+#pragma unroll
+        for (int k = 0; k < SPER; ++k) {
+            const int it = ts + k * kWinThreads;
+            const int tok = it / NCH, wc = it - tok * NCH;
+            const bool in = (SITEMS % kWinThreads == 0 || it < SITEMS) && (R == 64 || (tok >> 5) == hf);
+            *(u32x4 *)(in ? half + (tok - R * hf) * PITCH + 16 * wc : trash) = x[k];
+        }
+    };
+    // Rotates this wavefront's quads of the staged half into MFMA operands.
+    auto rotate_half = [&](u32x4 (&op)[S], int hf) {
+        const int tok = r + 32 * hf;
+        const float *crow = tab + tok * CS;
+        const char *xrow = half + (R == 64 ? tok : r) * PITCH + w * (2 * D);
 #pragma unroll
         for (int t = 0; t < S; ++t) {
             const int i = g * S + t;
-            const bool has = valid && i < NQ;
+            const bool has = tok < L && i < NQ;
             const int il = i < NQ ? i : 0;
-            u32x2 a0, a1, b0, b1;
-            load_rotate_quad<D, E, RD, FULL>(qrow, crow, srow, il, has, a0, a1);
-            load_rotate_quad<D, E, RD, FULL>(krow, crow, srow, il, has, b0, b1);
-            qop[tt][t] = u32x4{a0[0], a0[1], a1[0], a1[1]};
-            kop[tt][t] = u32x4{b0[0], b0[1], b1[0], b1[1]};
+            const f32x4 c0 = *(const f32x4 *)(crow + 4 * il);
+            const f32x4 s0v = *(const f32x4 *)(crow + W + 4 * il);
+            f32x4 c1 = c0, s1v = s0v;
+            if constexpr (FULL) {
+                c1 = *(const f32x4 *)(crow + D / 2 + 4 * il);
+                s1v = *(const f32x4 *)(crow + W + D / 2 + 4 * il);
+            }
+            u32x2 x0 = *(const u32x2 *)(xrow + 8 * il);
+            u32x2 x1 = *(const u32x2 *)(xrow + D + 8 * il);
+            if (!has) x0 = x1 = u32x2{0u, 0u};
+            u32x2 a0, a1;
+            rotate_quad<E>(x0, x1, c0, s0v, c1, s1v, a0, a1);
+            op[t] = u32x4{a0[0], a0[1], a1[0], a1[1]};
+        }
+    };
+    u32x4 qop[2][S], kop[2][S];
+    if constexpr (R == 64) {
+        stage_half(qs, 0);
+        __syncthreads();
+        rotate_half(qop[0], 0);
+        rotate_half(qop[1], 1);
+        __syncthreads();
+        // ---- 3. the K slab -----------------------------------------------------------
+        stage_half(ks, 0);
+        __syncthreads();
+        rotate_half(kop[0], 0);
+        rotate_half(kop[1], 1);
+    } else {
+        stage_half(qs, 0);
+        __syncthreads();
+        rotate_half(qop[0], 0);
+        __syncthreads();
+        stage_half(qs, 1);
+        __syncthreads();
+        rotate_half(qop[1], 1);
+        __syncthreads();
+        // ---- 3. the K slab -----------------------------------------------------------
+        stage_half(ks, 0);
+        __syncthreads();
+        rotate_half(kop[0], 0);
+        __syncthreads();
+        stage_half(ks, 1);
+        __syncthreads();
+        rotate_half(kop[1], 1);
+    }
+    __syncthreads();  // tables and the staged slab are dead: V^T goes over them
+
+    // ---- 4. V^T: vt[hh][d][j] = {V[2j][d], V[2j+1][d]} ------------------------------
+    t1 = fresh(tid);
+#pragma unroll
+    for (int k = 0; k < VPER; ++k) {
+        const int it = t1 + k * kWinThreads;
+        const bool in = VITEMS % kWinThreads == 0 || it < VITEMS;
+        const int itc = in ? it : 0;
+        const int j = itc / NCH, wc = itc - j * NCH;
+        const int hh = wc / HCH, c = wc - hh * HCH;
+        u32x4 A = va[k], B = vv[k];
+        if (2 * j >= L) A = u32x4{0u, 0u, 0u, 0u};
+        if (2 * j + 1 >= L) B = u32x4{0u, 0u, 0u, 0u};
+        // rho is a multiple of 8, so the item's 8 rows share one swizzle value
+        const int rho = hh * D + 8 * c;
+        u32 *col = vt_all + rho * VTS + (j ^ vswz(rho));
+        const int cs = in ? VTS : 0;  // out-of-range items write the trash slot 8 times
+        if (!in) col = (u32 *)trash;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            col[(2 * e) * cs] = perm(B[e], A[e], kSelLo);
+            col[(2 * e + 1) * cs] = perm(B[e], A[e], kSelHi);
         }
     }
     __syncthreads();
 
+    // ---- 5. attention per 32-query tile ---------------------------------------------
+    // The query-tile loop stays rolled (unrolled, the compiler overlaps the two
+    // tiles and runs out of registers); the tile's operands and results are
+    // selected with explicit selects, as a register array must not be indexed
+    // by the loop variable.
     const float sl = p.scale_log2;
     const int nkt = (L + 31) >> 5;
-#pragma unroll
+    const u32 *vt = vt_all + w * (D * VTS);
+    u32x2 outq[2][OQ];  // packed normalised output quads (q = 32b + r, d0 = 32dt + 8jq + 4g)
+#pragma unroll 1
     for (int b = 0; b < 2; ++b) {
-        if (b * 32 >= L) break;
+        __builtin_amdgcn_sched_barrier(0);
+        if (b * 32 >= L || !active) break;  // uniform within the wavefront; no barrier inside
+        u32x4 qcur[S];
+#pragma unroll
+        for (int t = 0; t < S; ++t) qcur[t] = b ? qop[1][t] : qop[0][t];
         // S^T tiles: rows kv, columns q.  Lane (r, g) holds q = 32b + r and
         // kv = 32a + 8(j/4) + 4g + (j%4) in element j of sacc[a].
         f32x16 sacc[2];
@@ -281,7 +472,7 @@ __global__ __launch_bounds__(64, 3) void window_kernel(const KParams p) {
             sacc[a] = f32x16{};
             if (a < nkt) {
 #pragma unroll
-                for (int t = 0; t < S; ++t) sacc[a] = E::mma(kop[a][t], qop[b][t], sacc[a]);
+                for (int t = 0; t < S; ++t) sacc[a] = E::mma(kop[a][t], qcur[t], sacc[a]);
             }
         }
         float mx = kNegInf;
@@ -307,6 +498,7 @@ __global__ __launch_bounds__(64, 3) void window_kernel(const KParams p) {
             }
         }
         lsum += xchg32(lsum);
+        const float inv = 1.0f / lsum;
 
         // P^T as the B operand of O^T = V^T P^T: step (a, h) uses elements
         // 8h..8h+7 of sacc[a], i.e. kv = 32a + 16h + {4g..4g+3, 8+4g..8+4g+3}.
@@ -320,41 +512,70 @@ __global__ __launch_bounds__(64, 3) void window_kernel(const KParams p) {
                                   E::pack(sacc[a][8 * h + 4], sacc[a][8 * h + 5]),
                                   E::pack(sacc[a][8 * h + 6], sacc[a][8 * h + 7])};
         }
-
-        // One 32-row d tile of O^T at a time, stored as soon as it is done.
-        // Element j of oacc: q = 32b + r, d = 32dt + 8(j/4) + 4g + (j%4).
-        const int q = 32 * b + r;
-        const float inv = 1.0f / lsum;
-        char *orow = p.out + ((int64_t)(s0 + q) * p.so_s + (int64_t)head * p.so_h) * 2;
+        // One 32-row d tile of O^T at a time; element j of oacc is
+        // q = 32b + r, d = 32dt + 8(j/4) + 4g + (j%4).
+        u32x2 ocur[OQ];
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
             const int d = 32 * dt + r;
-            const u32 *vrow = vt + min(d, D - 1) * VTS + 2 * g;
+            const int dr = min(d, D - 1);
+            const u32 *vrow = vt + dr * VTS;
+            const int xs = vswz(w * D + dr);
             f32x16 oacc = f32x16{};
 #pragma unroll
             for (int a = 0; a < 2; ++a) {
                 if (a >= nkt) break;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    const int kvh = 16 * a + 8 * h;  // dword column of kv = 32a + 16h + 4g, minus 2g
-                    const u32x2 lo = *(const u32x2 *)(vrow + kvh);
-                    const u32x2 hi = *(const u32x2 *)(vrow + kvh + 4);
+                    const int kc = 16 * a + 8 * h + 2 * g;  // dword column of kv = 32a + 16h + 4g
+                    const u32x2 lo = *(const u32x2 *)(vrow + (kc ^ xs));
+                    const u32x2 hi = *(const u32x2 *)(vrow + ((kc + 4) ^ xs));
                     u32x4 vop = {lo[0], lo[1], hi[0], hi[1]};
                     if (d >= D) vop = u32x4{0u, 0u, 0u, 0u};
                     oacc = E::mma(vop, pop[a][h], oacc);
                 }
             }
-            if (q < L) {
 #pragma unroll
-                for (int jq = 0; jq < 4; ++jq) {
-                    const int d0 = 32 * dt + 8 * jq + 4 * g;
-                    if (d0 < D) {
-                        const u32x2 w = {E::pack(oacc[4 * jq + 0] * inv, oacc[4 * jq + 1] * inv),
-                                         E::pack(oacc[4 * jq + 2] * inv, oacc[4 * jq + 3] * inv)};
-                        *(u32x2 *)(orow + 2 * d0) = w;
+            for (int jq = 0; jq < 4; ++jq)
+                ocur[4 * dt + jq] = u32x2{E::pack(oacc[4 * jq + 0] * inv, oacc[4 * jq + 1] * inv),
+                                          E::pack(oacc[4 * jq + 2] * inv, oacc[4 * jq + 3] * inv)};
+        }
+#pragma unroll
+        for (int i = 0; i < OQ; ++i) {
+            if (b) outq[1][i] = ocur[i];
+            else outq[0][i] = ocur[i];
+        }
+    }
+    __syncthreads();  // V^T is dead: the output rows go over it
+
+    // ---- 6. output rows through LDS, stored as coalesced slab rows --------------------
+    if (active) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if (b * 32 < L) {
+                char *orow = oslab + (32 * b + r) * PITCH + w * (2 * D);
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+                    for (int jq = 0; jq < 4; ++jq) {
+                        const int d0 = 32 * dt + 8 * jq + 4 * g;
+                        if (d0 < D) *(u32x2 *)(orow + 2 * d0) = outq[b][4 * dt + jq];
                     }
                 }
             }
+        }
+    }
+    __syncthreads();
+    const int to = fresh(tid);
+#pragma unroll
+    for (int k = 0; k < SPER; ++k) {
+        const int it = to + k * kWinThreads;
+        if (it < SITEMS) {
+            const int tok = it / NCH, wc = it - tok * NCH;
+            const int hh = wc / HCH, c = wc - hh * HCH;
+            if (tok < L && hh < nh)
+                *(u32x4 *)(ob + ((uint32_t)tok * ors + (uint32_t)hh * ohs + 16 * c)) =
+                    *(const u32x4 *)(oslab + tok * PITCH + 16 * wc);
         }
     }
 }
@@ -607,7 +828,7 @@ template <int D> bool pick_d(bool window, bool full, int qkv, int rd, Choice &c)
         else pick_rd<D, F16, FRA_DTYPE_F16>(window, full, c);
     }
     if (window) {
-        c.lds = 16 * ((D / 8 + 1) / 2) * 34 * 4;
+        c.lds = full ? WinLds<D, true>::kBytes : WinLds<D, false>::kBytes;
     } else {
         c.lds = LongLds<D>::kBytes;
     }
@@ -664,7 +885,11 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
     for (int i = 0; i < 9; ++i)
         if (strides[i] < 0) return fail(FRA_EINVAL, "strides must be >= 0");
 
-    const bool window = a->max_seqlen <= 64 && d <= kWindowMaxD;
+    // The window kernel addresses 64 rows of a tensor with 32-bit offsets.
+    const int64_t max_row_bytes = 2 * std::max(std::max(a->q_stride_seq, a->k_stride_seq),
+                                               std::max(a->v_stride_seq, a->out_stride_seq));
+    const bool small_rows = 64 * max_row_bytes < ((int64_t)1 << 31) && 64 * 4 * a->rope_stride_seq < ((int64_t)1 << 31);
+    const bool window = a->max_seqlen <= 64 && d <= kWindowMaxD && small_rows;
     memset(&c, 0, sizeof(c));
     if (!pick_kernel(d, window, a->rope_width == d, a->qkv_dtype, a->rope_dtype, c))
         return fail(FRA_EUNSUPPORTED, "head_dim=%d has no compiled kernel (built: 64, 72, 80, 96, 128)", d);
@@ -707,9 +932,9 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
     int64_t grid;
     if (window) {
         kp.qblocks = 1;
-        grid = sh;
+        grid = (int64_t)a->num_seqs * ((a->num_heads + kWinHeads - 1) / kWinHeads);
         c.kernel = FRA_KERNEL_WINDOW;
-        c.block = 64;
+        c.block = kWinThreads;
         c.block_q = 64;
         c.block_kv = 64;
         snprintf(c.name, sizeof(c.name), "window_d%d_%s_rope%s", d, dtype_name(a->qkv_dtype),

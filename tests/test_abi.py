@@ -66,7 +66,10 @@ def plan_of(a):
 def test_plan_window_and_long():
     rc, p = plan_of(make_args())
     assert rc == _lib.FRA_OK
-    assert p.kernel == _lib.FRA_KERNEL_WINDOW and p.grid == 16 * 16 and p.block == 64
+    # one workgroup of 4 wavefronts per (window, group of 4 heads)
+    assert p.kernel == _lib.FRA_KERNEL_WINDOW and p.grid == 16 * 4 and p.block == 256
+    rc, p = plan_of(make_args(h=6))  # a partial head group
+    assert rc == _lib.FRA_OK and p.grid == 16 * 2
     assert p.name.decode() == "window_d80_bf16_ropef32"
     rc, p = plan_of(make_args(max_seqlen=9216, num_seqs=1, n=9216))
     assert rc == _lib.FRA_OK and p.kernel == _lib.FRA_KERNEL_LONG
