@@ -175,7 +175,7 @@ def profile_driver(args, flush, dev) -> int:
     n = args.copy_mib << 20
     src = torch.ones(n // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
-    flush.fill_(1)
+    evict(flush)
     dst.copy_(src)
     torch.cuda.synchronize()
     n_tok, lens, nbytes, flops = workload_cost(w, inp)

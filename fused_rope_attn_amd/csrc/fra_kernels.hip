@@ -581,31 +581,59 @@ __global__ __launch_bounds__(kWinThreads, kWinWaves) void window_kernel(const KP
 }
 
 // ---- long kernel ----------------------------------------------------------------
+//
+// Split-Q flash tiling for segments of any length.  A workgroup of 4
+// wavefronts owns 128 query rows of one (segment, head) -- wavefront w rows
+// 32w..32w+31 -- and walks the segment's keys in blocks of 64:
+//
+//   * K_rot (rotated once per block, for all 128 rows) and V^T live in LDS,
+//     double-buffered; the next block's K/cos/sin/V are loaded into registers
+//     while the current block is computed, then rotated / transposed into the
+//     other buffer -- one barrier per block;
+//   * S^T = K_rot Q_rot^T on 32x32x16 MFMA (one query per lane column), exp2
+//     online softmax with the row max from v_max3 chains and one exchange
+//     with lane^32; the running max is only moved (and O rescaled) when a row
+//     max exceeds it by more than 2^8, so in the steady state no rescaling
+//     happens and P stays below 2^8;
+//   * O^T += V^T P^T; when head_dim leaves padding rows in the last 32-row
+//     tile of V^T, one of them holds ones, so the MFMA also produces the row
+//     sum of the rounded P (otherwise the sum is taken in fp32 on the VALU).
 
 constexpr int kLongBQ = 128;   // query rows per workgroup (4 waves x 32)
 constexpr int kLongBKV = 64;   // key/value rows per LDS stage
 constexpr int kLongThreads = 256;
+constexpr float kRescaleThreshold = 8.0f;  // log2 units
 
 template <int D> struct LongLds {
     static constexpr int DP = (D + 15) / 16 * 16;      // K_rot row padded to the MFMA k-step
-    static constexpr int KS = DP + 8;                  // K_rot row stride (elements), 16 B pad
+    static constexpr int KS = DP + 8;                  // K_rot row stride (bf16 elements), 16 B pad
     static constexpr int NDT = (D + 31) / 32;
     static constexpr int VTS = 36;                     // V^T row stride (dwords): 32 kv pairs + 4 pad
-    static constexpr int kBytes = kLongBKV * KS * 2 + NDT * 32 * VTS * 4;
+    static constexpr bool kOnesRow = D % 32 != 0;      // a padding row of V^T holds ones
+    static constexpr int kKBytes = kLongBKV * KS * 2;
+    static constexpr int kVBytes = NDT * 32 * VTS * 4;
+    static constexpr int kStage = kKBytes + kVBytes;   // one buffer
+    static constexpr int kBytes = 2 * kStage;
 };
 
 template <int D, class E, int RD, bool FULL>
-__global__ __launch_bounds__(kLongThreads) void long_kernel(const KParams p) {
+__global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) {
+    using LDS = LongLds<D>;
     constexpr int HALF = D / 2;
-    constexpr int NQ = D / 8;
-    constexpr int DP = LongLds<D>::DP;
+    constexpr int NQ = D / 8;                  // quads per half
+    constexpr int DP = LDS::DP;
     constexpr int S = DP / 16;
-    constexpr int KS = LongLds<D>::KS;
-    constexpr int NDT = LongLds<D>::NDT;
-    constexpr int VTS = LongLds<D>::VTS;
-    constexpr int NCH = D / 8;
-    __shared__ __attribute__((aligned(16))) u16 ks[kLongBKV * KS];
-    __shared__ __attribute__((aligned(16))) u32 vt[NDT * 32 * VTS];
+    constexpr int KS = LDS::KS;
+    constexpr int NDT = LDS::NDT;
+    constexpr int VTS = LDS::VTS;
+    constexpr int NCH = D / 8;                 // 16-byte chunks per V row
+    constexpr int RB = Rope<RD>::kBytes;
+    constexpr int KITEMS = kLongBKV * NQ;      // (row, quad) items of a K block
+    constexpr int KPER = (KITEMS + kLongThreads - 1) / kLongThreads;
+    constexpr int VITEMS = (kLongBKV / 4) * NCH;  // (kv quad, chunk) items of a V block
+    constexpr int VPER = (VITEMS + kLongThreads - 1) / kLongThreads;
+    constexpr bool ONES = LDS::kOnesRow;
+    __shared__ __attribute__((aligned(16))) char lds[LDS::kBytes];
 
     const int u = xcd_remap(blockIdx.x, gridDim.x);
     const int sh = u / p.qblocks, qblk = u - sh * p.qblocks;
@@ -617,16 +645,111 @@ __global__ __launch_bounds__(kLongThreads) void long_kernel(const KParams p) {
     if (L <= 0 || qblk * kLongBQ >= L) return;  // uniform across the workgroup
 
     const int tid = threadIdx.x;
-    const int w = tid >> 6, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int r = lane & 31, g = lane >> 5;
 
-    // Zero the K_rot pad columns [D, DP) and the V^T pad rows [D, 32*NDT):
-    // staging never writes them.
-    for (int i = tid; i < kLongBKV * (KS - D); i += kLongThreads) {
-        const int row = i / (KS - D), col = D + i % (KS - D);
-        ks[row * KS + col] = 0;
+    const char *kbase = p.k + ((int64_t)s0 * p.sk_s + (int64_t)head * p.sk_h) * 2;
+    const char *vbase = p.v + ((int64_t)s0 * p.sv_s + (int64_t)head * p.sv_h) * 2;
+    const char *cbase = p.cos + (int64_t)s0 * p.sr_s * RB;
+    const char *sbase = p.sin + (int64_t)s0 * p.sr_s * RB;
+    const int64_t krs = p.sk_s * 2, vrs = p.sv_s * 2, trs = p.sr_s * RB;
+
+    // Constant parts of both buffers: K_rot pad columns [D, DP) and V^T pad
+    // rows [D, 32*NDT) are zero (a ones row when it holds the row sum).
+    for (int bf = 0; bf < 2; ++bf) {
+        u16 *ks = (u16 *)(lds + bf * LDS::kStage);
+        u32 *vt = (u32 *)(lds + bf * LDS::kStage + LDS::kKBytes);
+        for (int i = tid; i < kLongBKV * (KS - D); i += kLongThreads) {
+            const int row = i / (KS - D), col = D + i % (KS - D);
+            ks[row * KS + col] = 0;
+        }
+        const u32 one = E::pack(1.0f, 1.0f);
+        for (int i = tid; i < (NDT * 32 - D) * VTS; i += kLongThreads)
+            vt[D * VTS + i] = (ONES && i < VTS) ? one : 0u;
     }
-    for (int i = tid; i < (NDT * 32 - D) * VTS; i += kLongThreads) vt[D * VTS + i] = 0u;
+
+    // ---- prefetch registers of one K/V block ------------------------------------
+    u32x2 kx0[KPER], kx1[KPER];
+    f32x4 kc0[KPER], ks0[KPER], kc1[KPER], ks1[KPER];
+    u32x4 vx[VPER][4];
+    auto load_block = [&](int kb) {
+        const int t = fresh(tid);
+#pragma unroll
+        for (int k = 0; k < KPER; ++k) {
+            const int it = min(t + k * kLongThreads, KITEMS - 1);
+            const int row = it / NQ, i = it - row * NQ;
+            const int tok = kb + row < L ? kb + row : 0;
+            const char *xr = kbase + tok * krs;
+            kx0[k] = *(const u32x2 *)(xr + 8 * i);
+            kx1[k] = *(const u32x2 *)(xr + 2 * HALF + 8 * i);
+            kc0[k] = Rope<RD>::quad(cbase + tok * trs + RB * 4 * i);
+            ks0[k] = Rope<RD>::quad(sbase + tok * trs + RB * 4 * i);
+            if constexpr (FULL) {
+                kc1[k] = Rope<RD>::quad(cbase + tok * trs + RB * (HALF + 4 * i));
+                ks1[k] = Rope<RD>::quad(sbase + tok * trs + RB * (HALF + 4 * i));
+            }
+        }
+        const int tv = fresh(tid);
+#pragma unroll
+        for (int k = 0; k < VPER; ++k) {
+            // kv quad fastest: the transposed LDS writes of a wavefront are then
+            // consecutive 8-byte columns of one V^T row
+            const int it = min(tv + k * kLongThreads, VITEMS - 1);
+            const int c = it / (kLongBKV / 4), kq = it - c * (kLongBKV / 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int tok = kb + 4 * kq + e < L ? kb + 4 * kq + e : 0;
+                vx[k][e] = *(const u32x4 *)(vbase + tok * vrs + 16 * c);
+            }
+        }
+    };
+    // Rotates / transposes the prefetched block into LDS buffer bf; rows past
+    // the segment become zeros.
+    auto store_block = [&](int kb, int bf) {
+        u16 *ks = (u16 *)(lds + bf * LDS::kStage);
+        u32 *vt = (u32 *)(lds + bf * LDS::kStage + LDS::kKBytes);
+        const int t = fresh(tid);
+#pragma unroll
+        for (int k = 0; k < KPER; ++k) {
+            const int it = t + k * kLongThreads;
+            const bool in = KITEMS % kLongThreads == 0 || it < KITEMS;
+            const int itc = in ? it : 0;
+            const int row = itc / NQ, i = itc - row * NQ;
+            u32x2 x0 = kx0[k], x1 = kx1[k];
+            if (kb + row >= L) x0 = x1 = u32x2{0u, 0u};
+            u32x2 r0w, r1w;
+            rotate_quad<E>(x0, x1, kc0[k], ks0[k], FULL ? kc1[k] : kc0[k], FULL ? ks1[k] : ks0[k], r0w, r1w);
+            if (in) {
+                *(u32x2 *)(ks + row * KS + 4 * i) = r0w;
+                *(u32x2 *)(ks + row * KS + HALF + 4 * i) = r1w;
+            }
+        }
+        const int tv = fresh(tid);
+#pragma unroll
+        for (int k = 0; k < VPER; ++k) {
+            const int it = tv + k * kLongThreads;
+            const bool in = VITEMS % kLongThreads == 0 || it < VITEMS;
+            const int itc = in ? it : 0;
+            const int c = itc / (kLongBKV / 4), kq = itc - c * (kLongBKV / 4);
+            u32x4 x[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[e] = vx[k][e];
+                if (kb + 4 * kq + e >= L) x[e] = u32x4{0u, 0u, 0u, 0u};
+            }
+            if (in) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    *(u32x2 *)(vt + (8 * c + 2 * j) * VTS + 2 * kq) =
+                        u32x2{perm(x[1][j], x[0][j], kSelLo), perm(x[3][j], x[2][j], kSelLo)};
+                    *(u32x2 *)(vt + (8 * c + 2 * j + 1) * VTS + 2 * kq) =
+                        u32x2{perm(x[1][j], x[0][j], kSelHi), perm(x[3][j], x[2][j], kSelHi)};
+                }
+            }
+        }
+    };
+
+    load_block(0);
 
     // Q_rot of this lane's query row, natural order [x0r | x1r | 0], as the
     // B operand of S^T: step t, group g takes elements 16t + 8g .. +7.
@@ -636,21 +759,27 @@ __global__ __launch_bounds__(kLongThreads) void long_kernel(const KParams p) {
         const bool valid = q < L;
         const int64_t row = s0 + (valid ? q : 0);
         const char *qrow = p.q + (row * p.sq_s + (int64_t)head * p.sq_h) * 2;
-        const char *crow = p.cos + row * p.sr_s * Rope<RD>::kBytes;
-        const char *srow = p.sin + row * p.sr_s * Rope<RD>::kBytes;
+        const char *crow = p.cos + row * p.sr_s * RB;
+        const char *srow = p.sin + row * p.sr_s * RB;
         u32x2 nat[DP / 4];  // natural quads: 0..NQ-1 = x0r, NQ..2NQ-1 = x1r, rest 0
 #pragma unroll
         for (int i = 0; i < NQ; ++i)
             load_rotate_quad<D, E, RD, FULL>(qrow, crow, srow, i, valid, nat[i], nat[NQ + i]);
 #pragma unroll
         for (int i = 2 * NQ; i < DP / 4; ++i) nat[i] = u32x2{0u, 0u};
+        // Bitwise select: a ?: on the two elements is folded into an index
+        // nat[4t + 2g] that would move the array to scratch memory.
+        const u32 msk = 0u - (u32)g;
 #pragma unroll
         for (int t = 0; t < S; ++t) {
-            const u32x2 a = g ? nat[4 * t + 2] : nat[4 * t];
-            const u32x2 b = g ? nat[4 * t + 3] : nat[4 * t + 1];
+            const u32x2 a = (nat[4 * t] & ~msk) | (nat[4 * t + 2] & msk);
+            const u32x2 b = (nat[4 * t + 1] & ~msk) | (nat[4 * t + 3] & msk);
             qop[t] = u32x4{a[0], a[1], b[0], b[1]};
         }
     }
+
+    store_block(0, 0);
+    __syncthreads();
 
     const float sl = p.scale_log2;
     float m_i = kNegInf, l_i = 0.f;
@@ -658,45 +787,16 @@ __global__ __launch_bounds__(kLongThreads) void long_kernel(const KParams p) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) oacc[dt] = f32x16{};
 
-    for (int kb = 0; kb < L; kb += kLongBKV) {
-        __syncthreads();  // the previous block's operands have been read
-        // Stage K_rot: item (row, quad i) rotates quad i of both halves.
-        for (int it = tid; it < kLongBKV * NQ; it += kLongThreads) {
-            const int row = it / NQ, i = it - row * NQ;
-            const int tok = kb + row;
-            const bool valid = tok < L;
-            const int64_t grow = s0 + (valid ? tok : 0);
-            const char *krow = p.k + (grow * p.sk_s + (int64_t)head * p.sk_h) * 2;
-            const char *crow = p.cos + grow * p.sr_s * Rope<RD>::kBytes;
-            const char *srow = p.sin + grow * p.sr_s * Rope<RD>::kBytes;
-            u32x2 r0w, r1w;
-            load_rotate_quad<D, E, RD, FULL>(krow, crow, srow, i, valid, r0w, r1w);
-            *(u32x2 *)(ks + row * KS + 4 * i) = r0w;
-            *(u32x2 *)(ks + row * KS + HALF + 4 * i) = r1w;
-        }
-        // Stage V^T: item (kv quad, 16-byte chunk c); vt[d][2kq..2kq+1]
-        // holds V[4kq..4kq+3][d].
-        for (int it = tid; it < (kLongBKV / 4) * NCH; it += kLongThreads) {
-            const int kq = it / NCH, c = it - kq * NCH;
-            u32x4 x[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int tok = kb + 4 * kq + e;
-                const bool valid = tok < L;
-                x[e] = *(const u32x4 *)(p.v + ((int64_t)(s0 + (valid ? tok : 0)) * p.sv_s + (int64_t)head * p.sv_h) * 2 +
-                                        16 * c);
-                if (!valid) x[e] = u32x4{0u, 0u, 0u, 0u};
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                *(u32x2 *)(vt + (8 * c + 2 * j) * VTS + 2 * kq) =
-                    u32x2{perm(x[1][j], x[0][j], kSelLo), perm(x[3][j], x[2][j], kSelLo)};
-                *(u32x2 *)(vt + (8 * c + 2 * j + 1) * VTS + 2 * kq) =
-                    u32x2{perm(x[1][j], x[0][j], kSelHi), perm(x[3][j], x[2][j], kSelHi)};
-            }
-        }
-        __syncthreads();
+    const int nblk = (L + kLongBKV - 1) / kLongBKV;
+    for (int j = 0; j < nblk; ++j) {
+        const int kb = j * kLongBKV;
+        const int bf = j & 1;
+        const bool more = j + 1 < nblk;
+        if (more) load_block(kb + kLongBKV);
+        __builtin_amdgcn_sched_barrier(0);
 
+        const u16 *ks = (const u16 *)(lds + bf * LDS::kStage);
+        const u32 *vt = (const u32 *)(lds + bf * LDS::kStage + LDS::kKBytes);
         const int nkv = min(kLongBKV, L - kb);
         const int nkt = (nkv + 31) >> 5;
         f32x16 sacc[2];
@@ -710,34 +810,45 @@ __global__ __launch_bounds__(kLongThreads) void long_kernel(const KParams p) {
                     sacc[a] = E::mma(*(const u32x4 *)(krow + 16 * t), qop[t], sacc[a]);
             }
         }
+        if (nkv < kLongBKV) {
+#pragma unroll
+            for (int a = 0; a < 2; ++a) {
+#pragma unroll
+                for (int jj = 0; jj < 16; ++jj) {
+                    const int kv = 32 * a + 8 * (jj >> 2) + 4 * g + (jj & 3);
+                    if (kv >= nkv) sacc[a][jj] = kNegInf;
+                }
+            }
+        }
         float mx = kNegInf;
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int kv = 32 * a + 8 * (j >> 2) + 4 * g + (j & 3);
-                if (kv >= nkv) sacc[a][j] = kNegInf;
-                mx = fmaxf(mx, sacc[a][j]);
-            }
+            for (int jj = 0; jj < 16; jj += 2)  // v_max3_f32
+                mx = fmaxf(mx, fmaxf(sacc[a][jj], sacc[a][jj + 1]));
         }
-        mx = fmaxf(mx, xchg32(mx));
-        const float m_new = fmaxf(m_i, mx * sl);
-        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+        mx = fmaxf(mx, xchg32(mx)) * sl;
+        // Lazy rescaling: move the running max only when it grows by more
+        // than the threshold (uniform branch over the wavefront).
+        if (__builtin_amdgcn_ballot_w64(mx > m_i + kRescaleThreshold) != 0) {
+            const float m_new = fmaxf(m_i, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
+            l_i *= alpha;
+            m_i = m_new;
+        }
         float lsum = 0.f;
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[a][j], sl, -m_new));
-                sacc[a][j] = e;
-                lsum += e;
+            for (int jj = 0; jj < 16; ++jj) {
+                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[a][jj], sl, -m_i));
+                sacc[a][jj] = e;
+                if constexpr (!ONES) lsum += e;
             }
         }
-        lsum += xchg32(lsum);
-        l_i = l_i * alpha + lsum;
-        m_i = m_new;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
+        if constexpr (!ONES) l_i += lsum + xchg32(lsum);
 
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
@@ -758,8 +869,19 @@ __global__ __launch_bounds__(kLongThreads) void long_kernel(const KParams p) {
                 }
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) store_block(kb + kLongBKV, bf ^ 1);
+        __syncthreads();
     }
 
+    if constexpr (ONES) {
+        // O^T row D (the ones row) is in element 4*((D % 32) / 8) of the last
+        // d tile, held by the g = 0 lanes.
+        constexpr int jl = 4 * ((D - 32 * (NDT - 1)) / 8);
+        const float lv = oacc[NDT - 1][jl];
+        const float lo = xchg32(lv);
+        l_i = g ? lo : lv;
+    }
     const int q = qblk * kLongBQ + 32 * w + r;
     if (q < L) {
         const float inv = 1.0f / l_i;
