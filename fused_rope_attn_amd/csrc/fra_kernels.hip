@@ -134,6 +134,14 @@ __device__ __forceinline__ float xchg32(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, x)));
 }
 
+// max(a, b, c) in one instruction (the compiler only forms v_max3_f32 under
+// no-NaN assumptions, which the -inf masking rules out).
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    float d;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+
 // An opaque copy of v: index arithmetic derived from it is recomputed in each
 // phase instead of being kept live (in registers) across the whole kernel.
 __device__ __forceinline__ int fresh(int v) {
@@ -582,26 +590,30 @@ __global__ __launch_bounds__(kWinThreads, kWinWaves) void window_kernel(const KP
 
 // ---- long kernel ----------------------------------------------------------------
 //
-// Split-Q flash tiling for segments of any length.  A workgroup of 4
-// wavefronts owns 128 query rows of one (segment, head) -- wavefront w rows
+// Split-Q flash tiling for segments of any length.  A workgroup of 8
+// wavefronts owns 256 query rows of one (segment, head) -- wavefront w rows
 // 32w..32w+31 -- and walks the segment's keys in blocks of 64:
 //
-//   * K_rot (rotated once per block, for all 128 rows) and V^T live in LDS,
+//   * K_rot (rotated once per block for all 256 rows) and V^T live in LDS,
 //     double-buffered; the next block's K/cos/sin/V are loaded into registers
 //     while the current block is computed, then rotated / transposed into the
-//     other buffer -- one barrier per block;
+//     other buffer -- one barrier per block.  Loads use a wave-uniform block
+//     base and 32-bit lane offsets computed once;
 //   * S^T = K_rot Q_rot^T on 32x32x16 MFMA (one query per lane column), exp2
 //     online softmax with the row max from v_max3 chains and one exchange
 //     with lane^32; the running max is only moved (and O rescaled) when a row
 //     max exceeds it by more than 2^8, so in the steady state no rescaling
 //     happens and P stays below 2^8;
-//   * O^T += V^T P^T; when head_dim leaves padding rows in the last 32-row
-//     tile of V^T, one of them holds ones, so the MFMA also produces the row
+//   * O^T += V^T P^T with the V^T columns of each 16-key group stored in the
+//     order the P^T k-slots visit them, so every A operand is one aligned
+//     16-byte LDS read; when head_dim leaves padding rows in the last 32-row
+//     tile of V^T, one of them holds ones and the MFMA also produces the row
 //     sum of the rounded P (otherwise the sum is taken in fp32 on the VALU).
 
-constexpr int kLongBQ = 128;   // query rows per workgroup (4 waves x 32)
-constexpr int kLongBKV = 64;   // key/value rows per LDS stage
-constexpr int kLongThreads = 256;
+constexpr int kLongWaves = 4;
+constexpr int kLongBQ = 32 * kLongWaves;  // query rows per workgroup
+constexpr int kLongBKV = 64;              // key/value rows per LDS stage
+constexpr int kLongThreads = 64 * kLongWaves;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
 
 template <int D> struct LongLds {
@@ -615,6 +627,14 @@ template <int D> struct LongLds {
     static constexpr int kStage = kKBytes + kVBytes;   // one buffer
     static constexpr int kBytes = 2 * kStage;
 };
+
+// Dword column of kv quad kq (keys 4kq..4kq+3) in a V^T row: within each
+// 16-key group the quads are stored in the order 0, 2, 1, 3, so the keys
+// lane group g feeds to a PV step ({4g..4g+3, 8+4g..8+4g+3}) are 4
+// consecutive dwords at column 8 * (group) + 4g.
+__device__ __forceinline__ int vt_quad_col(int kq) {
+    return 8 * (kq >> 2) + 2 * (((kq & 1) << 1) | ((kq >> 1) & 1));
+}
 
 template <int D, class E, int RD, bool FULL>
 __global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) {
@@ -668,81 +688,100 @@ __global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) 
             vt[D * VTS + i] = (ONES && i < VTS) ? one : 0u;
     }
 
+    // ---- per-thread staging items, fixed for the whole loop -------------------------
+    // K item k: (row, quad i); V item: (chunk c, kv quad kq), kv quad fastest so a
+    // wavefront's transposed LDS writes are consecutive columns of one V^T row.
+    int krow[KPER], kqd[KPER];
+    uint32_t koff[KPER], toff[KPER];
+#pragma unroll
+    for (int k = 0; k < KPER; ++k) {
+        const int it = min(tid + k * kLongThreads, KITEMS - 1);
+        krow[k] = it / NQ;
+        kqd[k] = it - krow[k] * NQ;
+        koff[k] = (uint32_t)(krow[k] * krs) + 8 * kqd[k];
+        toff[k] = (uint32_t)(krow[k] * trs) + RB * 4 * kqd[k];
+    }
+    int vkq[VPER], vch[VPER];
+    uint32_t voff[VPER];
+#pragma unroll
+    for (int k = 0; k < VPER; ++k) {
+        const int it = min(tid + k * kLongThreads, VITEMS - 1);
+        vch[k] = it / (kLongBKV / 4);
+        vkq[k] = it - vch[k] * (kLongBKV / 4);
+        voff[k] = (uint32_t)(4 * vkq[k] * vrs) + 16 * vch[k];
+    }
+    const uint32_t vrs32 = (uint32_t)vrs;
+
     // ---- prefetch registers of one K/V block ------------------------------------
     u32x2 kx0[KPER], kx1[KPER];
     f32x4 kc0[KPER], ks0[KPER], kc1[KPER], ks1[KPER];
     u32x4 vx[VPER][4];
+    // Rows of a partial last block past the segment read row 0 of the block
+    // (clamped offsets); their values are replaced by zeros when stored.
     auto load_block = [&](int kb) {
-        const int t = fresh(tid);
+        const bool full = kb + kLongBKV <= L;
+        const char *kblk = kbase + kb * krs, *vblk = vbase + kb * vrs;
+        const char *cblk = cbase + kb * trs, *sblk = sbase + kb * trs;
 #pragma unroll
         for (int k = 0; k < KPER; ++k) {
-            const int it = min(t + k * kLongThreads, KITEMS - 1);
-            const int row = it / NQ, i = it - row * NQ;
-            const int tok = kb + row < L ? kb + row : 0;
-            const char *xr = kbase + tok * krs;
-            kx0[k] = *(const u32x2 *)(xr + 8 * i);
-            kx1[k] = *(const u32x2 *)(xr + 2 * HALF + 8 * i);
-            kc0[k] = Rope<RD>::quad(cbase + tok * trs + RB * 4 * i);
-            ks0[k] = Rope<RD>::quad(sbase + tok * trs + RB * 4 * i);
+            const bool ok = full || kb + krow[k] < L;
+            const uint32_t ko = ok ? koff[k] : 8u * kqd[k];
+            const uint32_t to = ok ? toff[k] : (uint32_t)(RB * 4 * kqd[k]);
+            kx0[k] = *(const u32x2 *)(kblk + ko);
+            kx1[k] = *(const u32x2 *)(kblk + ko + 2 * HALF);
+            kc0[k] = Rope<RD>::quad(cblk + to);
+            ks0[k] = Rope<RD>::quad(sblk + to);
             if constexpr (FULL) {
-                kc1[k] = Rope<RD>::quad(cbase + tok * trs + RB * (HALF + 4 * i));
-                ks1[k] = Rope<RD>::quad(sbase + tok * trs + RB * (HALF + 4 * i));
+                kc1[k] = Rope<RD>::quad(cblk + to + RB * HALF);
+                ks1[k] = Rope<RD>::quad(sblk + to + RB * HALF);
             }
         }
-        const int tv = fresh(tid);
 #pragma unroll
         for (int k = 0; k < VPER; ++k) {
-            // kv quad fastest: the transposed LDS writes of a wavefront are then
-            // consecutive 8-byte columns of one V^T row
-            const int it = min(tv + k * kLongThreads, VITEMS - 1);
-            const int c = it / (kLongBKV / 4), kq = it - c * (kLongBKV / 4);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int tok = kb + 4 * kq + e < L ? kb + 4 * kq + e : 0;
-                vx[k][e] = *(const u32x4 *)(vbase + tok * vrs + 16 * c);
+                const bool ok = full || kb + 4 * vkq[k] + e < L;
+                const uint32_t vo = ok ? voff[k] + e * vrs32 : 16u * vch[k];
+                vx[k][e] = *(const u32x4 *)(vblk + vo);
             }
         }
     };
     // Rotates / transposes the prefetched block into LDS buffer bf; rows past
     // the segment become zeros.
     auto store_block = [&](int kb, int bf) {
+        const bool full = kb + kLongBKV <= L;
         u16 *ks = (u16 *)(lds + bf * LDS::kStage);
         u32 *vt = (u32 *)(lds + bf * LDS::kStage + LDS::kKBytes);
-        const int t = fresh(tid);
 #pragma unroll
         for (int k = 0; k < KPER; ++k) {
-            const int it = t + k * kLongThreads;
+            const int it = tid + k * kLongThreads;
             const bool in = KITEMS % kLongThreads == 0 || it < KITEMS;
-            const int itc = in ? it : 0;
-            const int row = itc / NQ, i = itc - row * NQ;
             u32x2 x0 = kx0[k], x1 = kx1[k];
-            if (kb + row >= L) x0 = x1 = u32x2{0u, 0u};
+            if (!full && kb + krow[k] >= L) x0 = x1 = u32x2{0u, 0u};
             u32x2 r0w, r1w;
             rotate_quad<E>(x0, x1, kc0[k], ks0[k], FULL ? kc1[k] : kc0[k], FULL ? ks1[k] : ks0[k], r0w, r1w);
             if (in) {
-                *(u32x2 *)(ks + row * KS + 4 * i) = r0w;
-                *(u32x2 *)(ks + row * KS + HALF + 4 * i) = r1w;
+                *(u32x2 *)(ks + krow[k] * KS + 4 * kqd[k]) = r0w;
+                *(u32x2 *)(ks + krow[k] * KS + HALF + 4 * kqd[k]) = r1w;
             }
         }
-        const int tv = fresh(tid);
 #pragma unroll
         for (int k = 0; k < VPER; ++k) {
-            const int it = tv + k * kLongThreads;
+            const int it = tid + k * kLongThreads;
             const bool in = VITEMS % kLongThreads == 0 || it < VITEMS;
-            const int itc = in ? it : 0;
-            const int c = itc / (kLongBKV / 4), kq = itc - c * (kLongBKV / 4);
             u32x4 x[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 x[e] = vx[k][e];
-                if (kb + 4 * kq + e >= L) x[e] = u32x4{0u, 0u, 0u, 0u};
+                if (!full && kb + 4 * vkq[k] + e >= L) x[e] = u32x4{0u, 0u, 0u, 0u};
             }
             if (in) {
+                u32 *col = vt + (8 * vch[k]) * VTS + vt_quad_col(vkq[k]);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    *(u32x2 *)(vt + (8 * c + 2 * j) * VTS + 2 * kq) =
+                    *(u32x2 *)(col + (2 * j) * VTS) =
                         u32x2{perm(x[1][j], x[0][j], kSelLo), perm(x[3][j], x[2][j], kSelLo)};
-                    *(u32x2 *)(vt + (8 * c + 2 * j + 1) * VTS + 2 * kq) =
+                    *(u32x2 *)(col + (2 * j + 1) * VTS) =
                         u32x2{perm(x[1][j], x[0][j], kSelHi), perm(x[3][j], x[2][j], kSelHi)};
                 }
             }
@@ -804,10 +843,10 @@ __global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) 
         for (int a = 0; a < 2; ++a) {
             sacc[a] = f32x16{};
             if (a < nkt) {
-                const u16 *krow = ks + (32 * a + r) * KS + 8 * g;
+                const u16 *krp = ks + (32 * a + r) * KS + 8 * g;
 #pragma unroll
                 for (int t = 0; t < S; ++t)
-                    sacc[a] = E::mma(*(const u32x4 *)(krow + 16 * t), qop[t], sacc[a]);
+                    sacc[a] = E::mma(*(const u32x4 *)(krp + 16 * t), qop[t], sacc[a]);
             }
         }
         if (nkv < kLongBKV) {
@@ -824,8 +863,7 @@ __global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) 
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
 #pragma unroll
-            for (int jj = 0; jj < 16; jj += 2)  // v_max3_f32
-                mx = fmaxf(mx, fmaxf(sacc[a][jj], sacc[a][jj + 1]));
+            for (int jj = 0; jj < 16; jj += 2) mx = max3f(mx, sacc[a][jj], sacc[a][jj + 1]);
         }
         mx = fmaxf(mx, xchg32(mx)) * sl;
         // Lazy rescaling: move the running max only when it grows by more
@@ -859,14 +897,10 @@ __global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) 
                                    E::pack(sacc[a][8 * h + 2], sacc[a][8 * h + 3]),
                                    E::pack(sacc[a][8 * h + 4], sacc[a][8 * h + 5]),
                                    E::pack(sacc[a][8 * h + 6], sacc[a][8 * h + 7])};
-                const int kvh = 16 * a + 8 * h + 2 * g;
+                const int kc = 8 * (2 * a + h) + 4 * g;  // the 16-key group's columns for group g
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) {
-                    const u32 *vrow = vt + (32 * dt + r) * VTS + kvh;
-                    const u32x2 lo = *(const u32x2 *)(vrow);
-                    const u32x2 hi = *(const u32x2 *)(vrow + 4);
-                    oacc[dt] = E::mma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pop, oacc[dt]);
-                }
+                for (int dt = 0; dt < NDT; ++dt)
+                    oacc[dt] = E::mma(*(const u32x4 *)(vt + (32 * dt + r) * VTS + kc), pop, oacc[dt]);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
