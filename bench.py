@@ -56,10 +56,30 @@ def workload_cost(w, inp):
     return n, lens, nbytes, flops
 
 
+def committed_traffic(workload: str, kernel: str):
+    """HBM bytes per call of ``kernel`` on ``workload`` from the committed
+    rocprofv3 summary ``profiles/<workload>_<kernel>.md`` (FETCH_SIZE and
+    WRITE_SIZE, each calibrated by a device copy of known size), or None when
+    no summary for this kernel is committed."""
+    path = os.path.join(ROOT, "profiles", f"{workload}_{kernel}.md")
+    if not os.path.exists(path):
+        return None
+    fields = {}
+    with open(path) as f:
+        for ln in f:
+            if ":" in ln and ln.startswith("- `"):
+                key, _, val = ln[3:].partition("`:")
+                fields[key.strip()] = val.strip().strip("`")
+    if fields.get("kernel") != kernel or "traffic_bytes_per_call" not in fields:
+        return None
+    return int(fields["traffic_bytes_per_call"])
+
+
 def evict(flush: torch.Tensor) -> None:
-    """Read the whole flush buffer: the caches end up holding its (clean)
-    lines instead of the workload's inputs."""
-    torch.sum(flush, dtype=torch.int32)
+    """Read the whole flush buffer with one reduction that converts nothing
+    (int64 elements, int64 sum): the caches end up holding its clean lines
+    instead of the workload's inputs, and no dirty lines are left behind."""
+    flush.view(torch.int64).sum()
 
 
 def measure(inp, steps: int, warmup: int, flush: torch.Tensor) -> dict:
@@ -179,9 +199,81 @@ def profile_driver(args, flush, dev) -> int:
     dst.copy_(src)
     torch.cuda.synchronize()
     n_tok, lens, nbytes, flops = workload_cost(w, inp)
-    print(json.dumps({"profile_driver": args.workload, "calls": args.profile_calls, "bytes": nbytes,
-                      "flops": flops, "copy_bytes_each_way": n}), flush=True)
+    pl = plan(q, k, v, cos, sin, cu, max_seqlen=inp["max_seqlen"])
+    print(json.dumps({"profile_driver": args.workload, "kernel": pl["name"], "warmup_calls": 3,
+                      "calls": args.profile_calls, "bytes": nbytes, "flops": flops,
+                      "copy_bytes_each_way": n}), flush=True)
     return 0
+
+
+def drift_stack(wname: str, device, layers: int = 32, full_layers=(7, 15, 23, 31), seed: int = 7) -> dict:
+    """Relative drift of a stack of attention layers run through the fused op
+    in bf16, against the same stack in fp32 on the CPU (the oracle).
+
+    Layer l normalises each token of ``x_l [N, H, D]`` to unit RMS (a
+    pre-norm block, which keeps the logits O(1) however far the residual
+    stream grows), maps it to q, k, v with seeded per-head ``D x D`` matrices
+    (scaled by ``1/sqrt(D)``) and adds the attention output:
+    ``x_{l+1} = x_l + attn_l(q, k, v)``.  Window layers use the workload's
+    window ``cu_seqlens``; layers in ``full_layers`` attend over the whole
+    image (the tokens stay in window order, as in the Qwen2.5-VL encoder).
+    The GPU stack keeps activations in bf16.  A third stack runs the oracle's
+    bf16 rounding model on the CPU: the drift any bf16 pipeline with these
+    rounding points has, i.e. the floor the GPU stack is compared with.
+    Returns per-layer ``||x - x_ref|| / ||x_ref||`` of both."""
+    import math
+
+    import numpy as np
+
+    from oracle import attention as A
+    from oracle.numerics import round_bf16
+
+    w = WORKLOADS[wname]
+    inp = make_inputs(w, seed=seed, device="cpu", heads=1)
+    cos, sin, cu_win = inp["cos"], inp["sin"], inp["cu_seqlens"]
+    n, h, d = int(cu_win[-1]), w.heads, w.head_dim
+    cu_full = torch.tensor([0, n], dtype=torch.int32)
+    g = torch.Generator().manual_seed(seed)
+    x0 = torch.randn(n, h, d, generator=g)
+    cos_np, sin_np = cos.float().numpy(), sin.float().numpy()
+    cos_d, sin_d = cos.to(device), sin.to(device)
+    xr = x0.numpy().copy()
+    xe = round_bf16(xr)
+    xg = x0.to(torch.bfloat16).to(device)
+    rows = []
+    for layer in range(layers):
+        wts = torch.randn(3, h, d, d, generator=g) / math.sqrt(d)
+        full = layer in full_layers
+        cu = cu_full if full else cu_win
+        cu_np = cu.numpy()
+        ms = int((cu[1:] - cu[:-1]).max())
+        wn = wts.numpy()
+        def rms(x):
+            return x / np.sqrt(np.mean(np.square(x), axis=(1, 2), keepdims=True) + np.float32(1e-6))
+
+        # fp32 reference
+        qkv = np.matmul(rms(xr).transpose(1, 0, 2)[None], wn).transpose(0, 2, 1, 3)
+        xr = xr + A.fused_rope_attention(qkv[0], qkv[1], qkv[2], cos_np, sin_np, cu_np, mode="fp32")
+        # bf16 rounding model
+        qkv = round_bf16(np.matmul(rms(xe).transpose(1, 0, 2)[None], wn).transpose(0, 2, 1, 3))
+        att = A.fused_rope_attention(qkv[0], qkv[1], qkv[2], cos_np, sin_np, cu_np, mode="bf16")
+        xe = round_bf16(xe + att)
+        # the fused op on the GPU (projections in fp32, activations stored in bf16)
+        xf = xg.float()
+        xf = xf * torch.rsqrt(xf.square().mean(dim=(1, 2), keepdim=True) + 1e-6)
+        qkv = torch.matmul(xf.transpose(0, 1)[None], wts.to(device)).transpose(1, 2)
+        qkv = qkv.to(torch.bfloat16).contiguous()
+        out = fused_rope_attention(qkv[0], qkv[1], qkv[2], cos_d, sin_d, cu.to(device), ms)
+        xg = (xg.float() + out.float()).to(torch.bfloat16)
+        ref_norm = float(np.linalg.norm(xr))
+        gpu = float(np.linalg.norm(xg.float().cpu().numpy() - xr)) / ref_norm
+        emu = float(np.linalg.norm(xe - xr)) / ref_norm
+        rows.append({"layer": layer, "kind": "full" if full else "window", "gpu_rel": gpu, "bf16_model_rel": emu})
+        print(f"[drift] layer {layer:2d} {'full  ' if full else 'window'} gpu {gpu:.3e}  bf16-model {emu:.3e}",
+              file=sys.stderr, flush=True)
+    return {"workload": wname, "layers": layers, "full_layers": list(full_layers), "tokens": n, "heads": h,
+            "head_dim": d, "per_layer": rows, "final_gpu_rel": rows[-1]["gpu_rel"],
+            "final_bf16_model_rel": rows[-1]["bf16_model_rel"]}
 
 
 def main() -> int:
@@ -197,6 +289,8 @@ def main() -> int:
                     help="profiling driver: run this many cold calls of --workload, then a plain "
                          "device copy of --copy-mib MiB (HBM counter calibration), and exit")
     ap.add_argument("--copy-mib", type=int, default=256)
+    ap.add_argument("--drift", default=None, metavar="FILE",
+                    help="run the 32-layer drift stack on --workload's grid and write the report to FILE")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -210,6 +304,13 @@ def main() -> int:
     flush = torch.ones(FLUSH_BYTES, dtype=torch.uint8, device=dev)
     if args.profile_calls:
         return profile_driver(args, flush, dev)
+    if args.drift:
+        rep = drift_stack(args.workload, dev)
+        with open(args.drift, "w") as f:
+            json.dump(rep, f, indent=1)
+        print(json.dumps({"drift": args.workload, "final_gpu_rel": rep["final_gpu_rel"],
+                          "final_bf16_model_rel": rep["final_bf16_model_rel"]}), flush=True)
+        return 0
 
     torch.cuda.synchronize()
     res, inp = run_workload(args.workload, args.steps, args.warmup, flush, dev)
@@ -231,7 +332,7 @@ def main() -> int:
                    "max_seqlen": res["max_seqlen"], "heads": w.heads, "head_dim": w.head_dim,
                    "qkv": "bf16 [N, H, D]", "rope": f"fp32 [N, {w.head_dim // 2}]",
                    "cache": "cold: 1 GiB read before each timed call", "parallelism": "single GPU"},
-        "roofline": dict(res["roofline"], traffic=None),
+        "roofline": dict(res["roofline"], traffic=committed_traffic(args.workload, res["kernel"])),
         "kernel": res["kernel"],
         "cold_p10_us": round(res["cold_p10_us"], 3),
         "cold_p90_us": round(res["cold_p90_us"], 3),

@@ -267,3 +267,20 @@ def test_workload_parity(device, name):
     pc = dict(case, q=case["q"][:, perm], k=case["k"][:, perm], v=case["v"][:, perm])
     out_p = run_gpu(pc, device)
     assert torch.equal(out_p, out[:, perm.to(out.device)])
+
+
+# ---- known answers (tests/golden/attention_kat.npz, float64 from the definition) ----
+
+_KAT = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "attention_kat.npz"))
+
+
+@pytest.mark.parametrize("name", sorted({k.split("/")[0] for k in _KAT.files}))
+def test_known_answers(device, name):
+    case = {x: torch.from_numpy(_KAT[f"{name}/{x}"]) for x in ("q", "k", "v", "cos", "sin", "cu_seqlens")}
+    for x in ("q", "k", "v"):
+        case[x] = case[x].to(torch.bfloat16)   # the fixture values are bf16-representable
+    cu = _KAT[f"{name}/cu_seqlens"]
+    case["max_seqlen"] = int((cu[1:] - cu[:-1]).max())
+    out = run_gpu(case, device, softmax_scale=float(_KAT[f"{name}/scale"][0]))
+    assert torch.equal(case["q"].float(), torch.from_numpy(_KAT[f"{name}/q"]))
+    assert_close(f32(out), _KAT[f"{name}/out"], MAX_ABS, MEAN_ABS, name)
