@@ -113,7 +113,7 @@ def main():
     cases = [  # (name, cu_seqlens, heads, head_dim, full-width tables, scale)
         ("ragged_d64_half", [0, 5, 5, 13, 14, 30], 2, 64, False, 64 ** -0.5),
         ("ragged_d80_full", [0, 9, 20], 3, 80, True, 80 ** -0.5),
-        ("window_d72_scale", [0, 3, 11, 64], 1, 72, False, 0.7),
+        ("window_d72_scale", [0, 3, 11, 64], 1, 72, False, 0.2),
         ("long_d80", [0, 70, 71], 1, 80, False, 80 ** -0.5),
     ]
     for name, cu, heads, d, full, scale in cases:

@@ -284,3 +284,6 @@ def test_known_answers(device, name):
     out = run_gpu(case, device, softmax_scale=float(_KAT[f"{name}/scale"][0]))
     assert torch.equal(case["q"].float(), torch.from_numpy(_KAT[f"{name}/q"]))
     assert_close(f32(out), _KAT[f"{name}/out"], MAX_ABS, MEAN_ABS, name)
+    emu = A.fused_rope_attention(*(_KAT[f"{name}/{x}"] for x in ("q", "k", "v", "cos", "sin", "cu_seqlens")),
+                                 softmax_scale=float(_KAT[f"{name}/scale"][0]), mode="bf16")
+    assert_close(f32(out), emu, EMU_MAX_ABS, EMU_MEAN_ABS, name + " vs bf16 model")
