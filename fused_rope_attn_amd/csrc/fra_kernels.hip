@@ -32,6 +32,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "fra.h"
 
@@ -591,68 +592,102 @@ __global__ __launch_bounds__(kWinThreads, kWinWaves) void window_kernel(const KP
 // ---- long kernel ----------------------------------------------------------------
 //
 // Split-Q flash tiling for segments of any length.  A workgroup of 8
-// wavefronts owns 256 query rows of one (segment, head) -- wavefront w rows
-// 32w..32w+31 -- and walks the segment's keys in blocks of 64:
+// wavefronts (two per SIMD) owns 256 query rows of one (segment, head) --
+// wavefront w rows 32w..32w+31 -- and walks the segment's keys in blocks of 64.
 //
-//   * K_rot (rotated once per block for all 256 rows) and V^T live in LDS,
-//     double-buffered; the next block's K/cos/sin/V are loaded into registers
-//     while the current block is computed, then rotated / transposed into the
-//     other buffer -- one barrier per block.  Loads use a wave-uniform block
-//     base and 32-bit lane offsets computed once;
-//   * S^T = K_rot Q_rot^T on 32x32x16 MFMA (one query per lane column), exp2
-//     online softmax with the row max from v_max3 chains and one exchange
-//     with lane^32; the running max is only moved (and O rescaled) when a row
-//     max exceeds it by more than 2^8, so in the steady state no rescaling
-//     happens and P stays below 2^8;
-//   * O^T += V^T P^T with the V^T columns of each 16-key group stored in the
-//     order the P^T k-slots visit them, so every A operand is one aligned
-//     16-byte LDS read; when head_dim leaves padding rows in the last 32-row
-//     tile of V^T, one of them holds ones and the MFMA also produces the row
-//     sum of the rounded P (otherwise the sum is taken in fp32 on the VALU).
+// Staging.  Raw K rows, their cos/sin rows and V rows go from HBM straight to
+// LDS (global_load_lds_dwordx4: lane l of an instruction writes the 16 bytes
+// at LDS base + 16 l).  Each instruction moves one 16-byte column of a 64-row
+// block -- lane = row -- so LDS holds every staged block column-major in
+// 16-byte chunks ([chunk][row][16 B]) and a lane's global offset is just
+// row * row_stride.  K is rotated from LDS into a row-major K_rot buffer once
+// per block for all 256 query rows (wavefront w takes quads w, w + 8, ... of
+// all 64 rows).  V stays as loaded; ds_read_b64_tr_b16 reads it back
+// transposed into the A operand of O^T = V^T P^T.
+//
+// Pipeline.  Iteration j overlaps matrix-core and vector work of one wavefront:
+//
+//     phase A:  S(j+1) = K_rot(j+1) Q_rot^T  (MFMA)   with  softmax of S(j)  (VALU)
+//     phase B:  O^T += V(j)^T P(j)^T          (MFMA)   with  rotation of K(j+2) (VALU)
+//
+// while the direct loads of raw K(j+3) (+cos/sin) and V(j+1) are in flight;
+// one barrier ends the iteration.  Buffers: K_rot and V double-buffered (block
+// x in buffer x & 1), raw K/cos/sin double-buffered when LDS allows (else one
+// buffer, K(j+2) loaded in iteration j, and a second barrier between the
+// phases).
+//
+// Softmax: exp2 online softmax with the row max from v_max3 chains and one
+// exchange with lane^32; the running max is only moved (and O rescaled) when a
+// row max exceeds it by more than 2^8, so in the steady state no rescaling
+// happens and P stays below 2^8.  When head_dim leaves padding columns in the
+// last 32-column tile of V, column D holds ones, so the PV MFMA also produces
+// the row sum of the rounded P (otherwise the sum is taken on the VALU).
+//
+// Rows of the last (partial) block past the segment load row nkv-1 instead
+// (finite values), and their scores are masked to -inf, so they add nothing.
+//
+// ds_read_b64_tr_b16 (gfx950) works on groups of 16 lanes: lane c of a group
+// supplies the address of a 4-element (8-byte) chunk, and lane i of the group
+// receives element (i & 3) of the chunks of lanes i/4, 4 + i/4, 8 + i/4 and
+// 12 + i/4.  With lane c = 4e + qq pointing at V[row0 + e][col0 + 4qq], lane i
+// receives V[row0 + 0..3][col0 + i]: four consecutive keys of column col0 + i.
 
-constexpr int kLongWaves = 4;
+constexpr int kLongWaves = 8;
 constexpr int kLongBQ = 32 * kLongWaves;  // query rows per workgroup
-constexpr int kLongBKV = 64;              // key/value rows per LDS stage
+constexpr int kLongBKV = 64;              // key/value rows per stage
 constexpr int kLongThreads = 64 * kLongWaves;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
+constexpr int kLdsLimit = 160 * 1024;
 
-template <int D> struct LongLds {
+template <int D, int RD, bool FULL> struct LongLds {
+    static constexpr int RB = RD == FRA_DTYPE_F32 ? 4 : 2;
+    static constexpr int HALF = D / 2;
+    static constexpr int W = FULL ? D : D / 2;         // table width
     static constexpr int DP = (D + 15) / 16 * 16;      // K_rot row padded to the MFMA k-step
-    static constexpr int KS = DP + 8;                  // K_rot row stride (bf16 elements), 16 B pad
-    static constexpr int NDT = (D + 31) / 32;
-    static constexpr int VTS = 36;                     // V^T row stride (dwords): 32 kv pairs + 4 pad
-    static constexpr bool kOnesRow = D % 32 != 0;      // a padding row of V^T holds ones
-    static constexpr int kKBytes = kLongBKV * KS * 2;
-    static constexpr int kVBytes = NDT * 32 * VTS * 4;
-    static constexpr int kStage = kKBytes + kVBytes;   // one buffer
-    static constexpr int kBytes = 2 * kStage;
+    static constexpr int KS = DP + 8;                  // K_rot row pitch (elements), 16 B pad
+    static constexpr int NDT = (D + 31) / 32;          // 32-row tiles of O^T
+    static constexpr int KCH = D / 8;                  // 16-byte chunks of a K or V row
+    static constexpr int TCH = W * RB / 16;            // 16-byte chunks of a table row
+    static constexpr int VCOLS = 4 * NDT;              // V chunk columns read by the MFMAs
+    static constexpr int CST = 64 * 16;                // chunk column stride, raw K and tables
+    static constexpr int VCST = 64 * 16 + 64;          // chunk column stride of V (bank offset 16)
+    static constexpr bool kOnesCol = D % 32 != 0;      // V column D holds ones
+    static constexpr int kRawK = KCH * CST;
+    static constexpr int kRawT = TCH * CST;
+    static constexpr int kRaw = kRawK + 2 * kRawT;     // raw K, cos, sin of one block
+    static constexpr int kKrot = kLongBKV * KS * 2;
+    static constexpr int kV = VCOLS * VCST;
+    static constexpr int kRawBufs = 2 * (kRaw + kKrot + kV) <= kLdsLimit ? 2 : 1;
+    static constexpr int kOffKrot = kRawBufs * kRaw;
+    static constexpr int kOffV = kOffKrot + 2 * kKrot;
+    static constexpr int kBytes = kOffV + 2 * kV;
+    static_assert(kBytes <= kLdsLimit, "long kernel LDS budget");
+    static_assert(W * RB % 16 == 0, "table rows must be whole 16-byte chunks");
 };
 
-// Dword column of kv quad kq (keys 4kq..4kq+3) in a V^T row: within each
-// 16-key group the quads are stored in the order 0, 2, 1, 3, so the keys
-// lane group g feeds to a PV step ({4g..4g+3, 8+4g..8+4g+3}) are 4
-// consecutive dwords at column 8 * (group) + 4g.
-__device__ __forceinline__ int vt_quad_col(int kq) {
-    return 8 * (kq >> 2) + 2 * (((kq & 1) << 1) | ((kq >> 1) & 1));
-}
-
 template <int D, class E, int RD, bool FULL>
-__global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) {
-    using LDS = LongLds<D>;
+__global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) {
+    using LDS = LongLds<D, RD, FULL>;
     constexpr int HALF = D / 2;
     constexpr int NQ = D / 8;                  // quads per half
     constexpr int DP = LDS::DP;
     constexpr int S = DP / 16;
     constexpr int KS = LDS::KS;
     constexpr int NDT = LDS::NDT;
-    constexpr int VTS = LDS::VTS;
-    constexpr int NCH = D / 8;                 // 16-byte chunks per V row
-    constexpr int RB = Rope<RD>::kBytes;
-    constexpr int KITEMS = kLongBKV * NQ;      // (row, quad) items of a K block
-    constexpr int KPER = (KITEMS + kLongThreads - 1) / kLongThreads;
-    constexpr int VITEMS = (kLongBKV / 4) * NCH;  // (kv quad, chunk) items of a V block
-    constexpr int VPER = (VITEMS + kLongThreads - 1) / kLongThreads;
-    constexpr bool ONES = LDS::kOnesRow;
+    constexpr int RB = LDS::RB;
+    constexpr int KCH = LDS::KCH, TCH = LDS::TCH;
+    constexpr int CST = LDS::CST, VCST = LDS::VCST;
+    constexpr int NRAWI = KCH + 2 * TCH;       // direct loads of one raw block
+    constexpr int NDMA = NRAWI + KCH;          // ... plus the V block
+    constexpr int MPER = (NDMA + kLongWaves - 1) / kLongWaves;
+    constexpr int RPER = (NQ + kLongWaves - 1) / kLongWaves;  // rotation quads per wavefront
+    constexpr bool ONES = LDS::kOnesCol;
+    constexpr int RAWBUFS = LDS::kRawBufs;
+    constexpr int DIST = RAWBUFS + 1;          // raw K of block j + DIST is loaded in iteration j
+    typedef short v4i16 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+    typedef __attribute__((address_space(3))) void lds_void;
+    typedef __attribute__((address_space(1))) void glb_void;
     __shared__ __attribute__((aligned(16))) char lds[LDS::kBytes];
 
     const int u = xcd_remap(blockIdx.x, gridDim.x);
@@ -667,6 +702,7 @@ __global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int r = lane & 31, g = lane >> 5;
+    const int nblk = (L + kLongBKV - 1) / kLongBKV;
 
     const char *kbase = p.k + ((int64_t)s0 * p.sk_s + (int64_t)head * p.sk_h) * 2;
     const char *vbase = p.v + ((int64_t)s0 * p.sv_s + (int64_t)head * p.sv_h) * 2;
@@ -674,121 +710,134 @@ __global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) 
     const char *sbase = p.sin + (int64_t)s0 * p.sr_s * RB;
     const int64_t krs = p.sk_s * 2, vrs = p.sv_s * 2, trs = p.sr_s * RB;
 
-    // Constant parts of both buffers: K_rot pad columns [D, DP) and V^T pad
-    // rows [D, 32*NDT) are zero (a ones row when it holds the row sum).
-    for (int bf = 0; bf < 2; ++bf) {
-        u16 *ks = (u16 *)(lds + bf * LDS::kStage);
-        u32 *vt = (u32 *)(lds + bf * LDS::kStage + LDS::kKBytes);
-        for (int i = tid; i < kLongBKV * (KS - D); i += kLongThreads) {
-            const int row = i / (KS - D), col = D + i % (KS - D);
-            ks[row * KS + col] = 0;
+    // V padding columns [D, 32*NDT) of both buffers: zero, column D ones.
+    // They are never overwritten by the staging loads.
+    {
+        constexpr int PADC = LDS::VCOLS - KCH;  // padding chunk columns
+        const u32 one = E::pack(1.0f, 0.0f) & 0xffffu;
+        for (int i = tid; i < 2 * PADC * 64; i += kLongThreads) {
+            const int bf = i / (PADC * 64), rem = i - bf * PADC * 64;
+            const int pc = rem / 64, row = rem - pc * 64;
+            u32x4 val = {0u, 0u, 0u, 0u};
+            if (ONES && pc == 0) val[0] = one;  // element 0 of chunk D/8 is column D
+            *(u32x4 *)(lds + LDS::kOffV + bf * LDS::kV + (KCH + pc) * VCST + row * 16) = val;
         }
-        const u32 one = E::pack(1.0f, 1.0f);
-        for (int i = tid; i < (NDT * 32 - D) * VTS; i += kLongThreads)
-            vt[D * VTS + i] = (ONES && i < VTS) ? one : 0u;
     }
 
-    // ---- per-thread staging items, fixed for the whole loop -------------------------
-    // K item k: (row, quad i); V item: (chunk c, kv quad kq), kv quad fastest so a
-    // wavefront's transposed LDS writes are consecutive columns of one V^T row.
-    int krow[KPER], kqd[KPER];
-    uint32_t koff[KPER], toff[KPER];
-#pragma unroll
-    for (int k = 0; k < KPER; ++k) {
-        const int it = min(tid + k * kLongThreads, KITEMS - 1);
-        krow[k] = it / NQ;
-        kqd[k] = it - krow[k] * NQ;
-        koff[k] = (uint32_t)(krow[k] * krs) + 8 * kqd[k];
-        toff[k] = (uint32_t)(krow[k] * trs) + RB * 4 * kqd[k];
-    }
-    int vkq[VPER], vch[VPER];
-    uint32_t voff[VPER];
-#pragma unroll
-    for (int k = 0; k < VPER; ++k) {
-        const int it = min(tid + k * kLongThreads, VITEMS - 1);
-        vch[k] = it / (kLongBKV / 4);
-        vkq[k] = it - vch[k] * (kLongBKV / 4);
-        voff[k] = (uint32_t)(4 * vkq[k] * vrs) + 16 * vch[k];
-    }
-    const uint32_t vrs32 = (uint32_t)vrs;
-
-    // ---- prefetch registers of one K/V block ------------------------------------
-    u32x2 kx0[KPER], kx1[KPER];
-    f32x4 kc0[KPER], ks0[KPER], kc1[KPER], ks1[KPER];
-    u32x4 vx[VPER][4];
-    // Rows of a partial last block past the segment read row 0 of the block
-    // (clamped offsets); their values are replaced by zeros when stored.
-    auto load_block = [&](int kb) {
-        const bool full = kb + kLongBKV <= L;
-        const char *kblk = kbase + kb * krs, *vblk = vbase + kb * vrs;
-        const char *cblk = cbase + kb * trs, *sblk = sbase + kb * trs;
-#pragma unroll
-        for (int k = 0; k < KPER; ++k) {
-            const bool ok = full || kb + krow[k] < L;
-            const uint32_t ko = ok ? koff[k] : 8u * kqd[k];
-            const uint32_t to = ok ? toff[k] : (uint32_t)(RB * 4 * kqd[k]);
-            kx0[k] = *(const u32x2 *)(kblk + ko);
-            kx1[k] = *(const u32x2 *)(kblk + ko + 2 * HALF);
-            kc0[k] = Rope<RD>::quad(cblk + to);
-            ks0[k] = Rope<RD>::quad(sblk + to);
-            if constexpr (FULL) {
-                kc1[k] = Rope<RD>::quad(cblk + to + RB * HALF);
-                ks1[k] = Rope<RD>::quad(sblk + to + RB * HALF);
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < VPER; ++k) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const bool ok = full || kb + 4 * vkq[k] + e < L;
-                const uint32_t vo = ok ? voff[k] + e * vrs32 : 16u * vch[k];
-                vx[k][e] = *(const u32x4 *)(vblk + vo);
-            }
-        }
+    // ---- direct-load jobs ---------------------------------------------------------
+    // A block is staged by NDMA direct loads, each moving one 16-byte chunk
+    // column of its 64 rows: raw K columns, cos columns, sin columns (the raw
+    // part), then V columns.  Wavefront w owns loads w, w + 8, ... (job m is
+    // load w + 8m).  Iteration j loads the raw part of block j + DIST and the
+    // V part of block j + 1.
+    constexpr int MFULL = NDMA / kLongWaves;  // jobs every wavefront has
+    struct Job {
+        const char *base;  // the job's chunk column in block 0
+        uint32_t rows;     // row stride (bytes)
+        uint32_t lds0;     // LDS destination in buffer 0
+        uint32_t bufstep;  // bytes between LDS buffers
+        bool raw;          // raw part (K, cos, sin) or V
     };
-    // Rotates / transposes the prefetched block into LDS buffer bf; rows past
-    // the segment become zeros.
-    auto store_block = [&](int kb, int bf) {
-        const bool full = kb + kLongBKV <= L;
-        u16 *ks = (u16 *)(lds + bf * LDS::kStage);
-        u32 *vt = (u32 *)(lds + bf * LDS::kStage + LDS::kKBytes);
-#pragma unroll
-        for (int k = 0; k < KPER; ++k) {
-            const int it = tid + k * kLongThreads;
-            const bool in = KITEMS % kLongThreads == 0 || it < KITEMS;
-            u32x2 x0 = kx0[k], x1 = kx1[k];
-            if (!full && kb + krow[k] >= L) x0 = x1 = u32x2{0u, 0u};
-            u32x2 r0w, r1w;
-            rotate_quad<E>(x0, x1, kc0[k], ks0[k], FULL ? kc1[k] : kc0[k], FULL ? ks1[k] : ks0[k], r0w, r1w);
-            if (in) {
-                *(u32x2 *)(ks + krow[k] * KS + 4 * kqd[k]) = r0w;
-                *(u32x2 *)(ks + krow[k] * KS + HALF + 4 * kqd[k]) = r1w;
-            }
+    auto job_desc = [&](int m) {
+        const int gi = min(w + kLongWaves * m, NDMA - 1);
+        Job jb;
+        if (gi < KCH) {
+            jb.base = kbase + 16 * gi;
+            jb.rows = (uint32_t)krs;
+            jb.lds0 = (uint32_t)(gi * CST);
+        } else if (gi < NRAWI) {
+            const bool is_cos = gi < KCH + TCH;
+            const int c = is_cos ? gi - KCH : gi - KCH - TCH;
+            jb.base = (is_cos ? cbase : sbase) + 16 * c;
+            jb.rows = (uint32_t)trs;
+            jb.lds0 = (uint32_t)(LDS::kRawK + (is_cos ? 0 : LDS::kRawT) + c * CST);
+        } else {
+            const int c = gi - NRAWI;
+            jb.base = vbase + 16 * c;
+            jb.rows = (uint32_t)vrs;
+            jb.lds0 = (uint32_t)(LDS::kOffV + c * VCST);
         }
+        jb.raw = gi < NRAWI;
+        jb.bufstep = jb.raw ? LDS::kRaw : LDS::kV;
+        return jb;
+    };
+    // Does this wavefront have job m?
+    auto has_job = [&](int m) { return m < MFULL || w + kLongWaves * m < NDMA; };
+    // Job m for block x (raw part: block xr into buffer br; V: block xv into
+    // buffer bv), the rows of a partial block clamped to its last row.
+    // Generic path: prologue and last iterations.
+    auto job_generic = [&](int m, int xr, int br, int xv, int bv) {
+        if (!has_job(m)) return;
+        const Job jb = job_desc(m);
+        const int x = jb.raw ? xr : xv, bf = jb.raw ? br : bv;
+        if (x >= nblk) return;
+        const int nkv = min(kLongBKV, L - kLongBKV * x);
+        const uint32_t voff = (uint32_t)min(lane, nkv - 1) * jb.rows;
+        const char *src = jb.base + (int64_t)x * kLongBKV * jb.rows;
+        __builtin_amdgcn_global_load_lds((glb_void *)(src + voff), (lds_void *)(lds + jb.lds0 + bf * jb.bufstep),
+                                         16, 0, 0);
+    };
+    // The loads of iteration j (generic path).
+    auto dma_iter = [&](int j) {
 #pragma unroll
-        for (int k = 0; k < VPER; ++k) {
-            const int it = tid + k * kLongThreads;
-            const bool in = VITEMS % kLongThreads == 0 || it < VITEMS;
-            u32x4 x[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x[e] = vx[k][e];
-                if (!full && kb + 4 * vkq[k] + e >= L) x[e] = u32x4{0u, 0u, 0u, 0u};
-            }
-            if (in) {
-                u32 *col = vt + (8 * vch[k]) * VTS + vt_quad_col(vkq[k]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    *(u32x2 *)(col + (2 * j) * VTS) =
-                        u32x2{perm(x[1][j], x[0][j], kSelLo), perm(x[3][j], x[2][j], kSelLo)};
-                    *(u32x2 *)(col + (2 * j + 1) * VTS) =
-                        u32x2{perm(x[1][j], x[0][j], kSelHi), perm(x[3][j], x[2][j], kSelHi)};
-                }
-            }
-        }
+        for (int m = 0; m < MPER; ++m) job_generic(m, j + DIST, (j + DIST) % RAWBUFS, j + 1, (j + 1) & 1);
+    };
+    // Steady state: running pointers (block j + DIST or j + 1 in iteration j),
+    // full blocks, the LDS destination fixed by the iteration parity P.
+    const char *jptr[MPER];
+    uint32_t jstep[MPER], jdst[MPER][2], jvoff[MPER];
+    auto job_steady = [&](int m, int P) {
+        __builtin_amdgcn_global_load_lds((glb_void *)(jptr[m] + jvoff[m]), (lds_void *)(lds + jdst[m][P]), 16, 0, 0);
+        jptr[m] += jstep[m];
     };
 
-    load_block(0);
+    // ---- rotation of one raw block into K_rot ---------------------------------------
+    // Wavefront w rotates quads i = w, w + 8, ... of row `lane`: fp32 math with
+    // separately rounded products (reference fused_attn.py:385-390), rounded to
+    // the storage dtype.  Quad w exists for every wavefront (NQ >= 8); the
+    // later ones only for some.
+    auto rotate_one = [&](int rawbuf, int kbuf, int i) {
+        const char *raw = lds + rawbuf * LDS::kRaw;
+        const char *ct = raw + LDS::kRawK, *st = raw + LDS::kRawK + LDS::kRawT;
+        char *kr = lds + LDS::kOffKrot + kbuf * LDS::kKrot + lane * (KS * 2);
+        // byte offset within a row -> (chunk column, byte within chunk)
+        auto at = [&](const char *base, int byte) { return base + (byte >> 4) * CST + lane * 16 + (byte & 15); };
+        const u32x2 x0 = *(const u32x2 *)at(raw, 8 * i);
+        const u32x2 x1 = *(const u32x2 *)at(raw, D + 8 * i);
+        const f32x4 c0 = Rope<RD>::quad(at(ct, RB * 4 * i));
+        const f32x4 s0v = Rope<RD>::quad(at(st, RB * 4 * i));
+        f32x4 c1 = c0, s1v = s0v;
+        if constexpr (FULL) {
+            c1 = Rope<RD>::quad(at(ct, RB * (HALF + 4 * i)));
+            s1v = Rope<RD>::quad(at(st, RB * (HALF + 4 * i)));
+        }
+        u32x2 r0w, r1w;
+        rotate_quad<E>(x0, x1, c0, s0v, c1, s1v, r0w, r1w);
+        *(u32x2 *)(kr + 8 * i) = r0w;
+        *(u32x2 *)(kr + D + 8 * i) = r1w;
+    };
+    static_assert(NQ >= kLongWaves, "every wavefront rotates at least one quad");
+    auto rotate_rest = [&](int rawbuf, int kbuf) {
+#pragma unroll
+        for (int m = 1; m < RPER; ++m) {
+            const int i = w + kLongWaves * m;
+            if (i < NQ) rotate_one(rawbuf, kbuf, i);
+        }
+    };
+    auto rotate = [&](int rawbuf, int kbuf) {
+        rotate_one(rawbuf, kbuf, w);
+        rotate_rest(rawbuf, kbuf);
+    };
+
+    auto wait_dma = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+
+    // ---- prologue -----------------------------------------------------------------
+    // raw K(0), V(0), and raw K(1) when there are two raw buffers
+#pragma unroll
+    for (int m = 0; m < MPER; ++m) {
+        job_generic(m, 0, 0, 0, 0);
+        if (RAWBUFS == 2) job_generic(m, 1, 1, nblk, 0);
+    }
 
     // Q_rot of this lane's query row, natural order [x0r | x1r | 0], as the
     // B operand of S^T: step t, group g takes elements 16t + 8g .. +7.
@@ -816,9 +865,38 @@ __global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) 
             qop[t] = u32x4{a[0], a[1], b[0], b[1]};
         }
     }
-
-    store_block(0, 0);
+    // K_rot zero padding columns [D, KS) of both buffers.
+    for (int i = tid; i < 2 * kLongBKV * (KS - D); i += kLongThreads) {
+        const int bf = i / (kLongBKV * (KS - D)), rem = i - bf * kLongBKV * (KS - D);
+        const int row = rem / (KS - D), col = D + rem % (KS - D);
+        *(u16 *)(lds + LDS::kOffKrot + bf * LDS::kKrot + (row * KS + col) * 2) = 0;
+    }
+    wait_dma();
     __syncthreads();
+    rotate(0, 0);
+    if constexpr (RAWBUFS == 2) {
+        if (nblk > 1) rotate(1, 1);
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < MPER; ++m) job_generic(m, 2, 0, nblk, 0);  // raw K(2)
+    } else {
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < MPER; ++m) job_generic(m, 1, 0, nblk, 0);  // raw K(1)
+        wait_dma();
+        __syncthreads();
+        if (nblk > 1) rotate(0, 1);
+        __syncthreads();
+    }
+
+    // Per-lane LDS byte offsets.  K_rot A operand of S^T: row 32a + r, elements
+    // 16t + 8g.  V transposed reads: the 16-lane group G = lane >> 4 covers
+    // keys 4g + e (e = (lane >> 2) & 3) and columns 16 (G & 1) + 4 (lane & 3) of
+    // each 32-column tile; column c lives in chunk c / 8 at byte 2 (c % 8).
+    const uint32_t k_lane = (uint32_t)(LDS::kOffKrot + (r * KS + 8 * g) * 2);
+    const int vcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const uint32_t v_lane =
+        (uint32_t)(LDS::kOffV + (vcol >> 3) * VCST + (4 * g + ((lane >> 2) & 3)) * 16 + (vcol & 7) * 2);
 
     const float sl = p.scale_log2;
     float m_i = kNegInf, l_i = 0.f;
@@ -826,29 +904,23 @@ __global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) 
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) oacc[dt] = f32x16{};
 
-    const int nblk = (L + kLongBKV - 1) / kLongBKV;
-    for (int j = 0; j < nblk; ++j) {
-        const int kb = j * kLongBKV;
-        const int bf = j & 1;
-        const bool more = j + 1 < nblk;
-        if (more) load_block(kb + kLongBKV);
-        __builtin_amdgcn_sched_barrier(0);
-
-        const u16 *ks = (const u16 *)(lds + bf * LDS::kStage);
-        const u32 *vt = (const u32 *)(lds + bf * LDS::kStage + LDS::kKBytes);
-        const int nkv = min(kLongBKV, L - kb);
-        const int nkt = (nkv + 31) >> 5;
-        f32x16 sacc[2];
+    // S^T of block x (K_rot buffer x & 1).
+    auto qk = [&](int x, f32x16 (&sacc)[2]) {
+        const char *kb = lds + k_lane + (x & 1) * LDS::kKrot;
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
-            sacc[a] = f32x16{};
-            if (a < nkt) {
-                const u16 *krp = ks + (32 * a + r) * KS + 8 * g;
+            sacc[a] = E::mma(*(const u32x4 *)(kb + a * (32 * KS * 2)), qop[0], f32x16{});
 #pragma unroll
-                for (int t = 0; t < S; ++t)
-                    sacc[a] = E::mma(*(const u32x4 *)(krp + 16 * t), qop[t], sacc[a]);
-            }
+            for (int t = 1; t < S; ++t)
+                sacc[a] = E::mma(*(const u32x4 *)(kb + a * (32 * KS * 2) + 32 * t), qop[t], sacc[a]);
         }
+    };
+
+    // Online softmax of one block's S^T, in two parts.  smax: masks keys
+    // past the segment (nkv < 64), takes the row max and moves the running
+    // max when needed (lazy rescaling: only when the row max grows by more
+    // than the threshold; a uniform branch over the wavefront).
+    auto smax = [&](f32x16 (&sacc)[2], int nkv) {
         if (nkv < kLongBKV) {
 #pragma unroll
             for (int a = 0; a < 2; ++a) {
@@ -859,15 +931,18 @@ __global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) 
                 }
             }
         }
-        float mx = kNegInf;
+        // Row max as a tree of v_max3 (short dependency chains).
+        float t[11];
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
-#pragma unroll
-            for (int jj = 0; jj < 16; jj += 2) mx = max3f(mx, sacc[a][jj], sacc[a][jj + 1]);
+        for (int k = 0; k < 10; ++k) {
+            const int e = 3 * k;
+            t[k] = max3f(sacc[e >> 4][e & 15], sacc[(e + 1) >> 4][(e + 1) & 15], sacc[(e + 2) >> 4][(e + 2) & 15]);
         }
+        t[10] = fmaxf(sacc[1][14], sacc[1][15]);
+        const float u0 = max3f(t[0], t[1], t[2]), u1 = max3f(t[3], t[4], t[5]);
+        const float u2 = max3f(t[6], t[7], t[8]), u3 = fmaxf(t[9], t[10]);
+        float mx = fmaxf(max3f(u0, u1, u2), u3);
         mx = fmaxf(mx, xchg32(mx)) * sl;
-        // Lazy rescaling: move the running max only when it grows by more
-        // than the threshold (uniform branch over the wavefront).
         if (__builtin_amdgcn_ballot_w64(mx > m_i + kRescaleThreshold) != 0) {
             const float m_new = fmaxf(m_i, mx);
             const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
@@ -876,6 +951,11 @@ __global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) 
             l_i *= alpha;
             m_i = m_new;
         }
+    };
+    // sexp: P = exp2(S * scale * log2e - m), packed as the B operands of the
+    // four PV steps.  Step (a, h) covers keys 32a + 16h + {4g..4g+3,
+    // 8+4g..8+4g+3}: elements 8h..8h+7 of sacc[a].
+    auto sexp = [&](f32x16 (&sacc)[2], u32x4 (&pop)[4]) {
         float lsum = 0.f;
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
@@ -887,30 +967,116 @@ __global__ __launch_bounds__(kLongThreads, 2) void long_kernel(const KParams p) 
             }
         }
         if constexpr (!ONES) l_i += lsum + xchg32(lsum);
-
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
-            if (a >= nkt) break;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const u32x4 pop = {E::pack(sacc[a][8 * h + 0], sacc[a][8 * h + 1]),
-                                   E::pack(sacc[a][8 * h + 2], sacc[a][8 * h + 3]),
-                                   E::pack(sacc[a][8 * h + 4], sacc[a][8 * h + 5]),
-                                   E::pack(sacc[a][8 * h + 6], sacc[a][8 * h + 7])};
-                const int kc = 8 * (2 * a + h) + 4 * g;  // the 16-key group's columns for group g
+            for (int h = 0; h < 2; ++h)
+                pop[2 * a + h] = u32x4{E::pack(sacc[a][8 * h + 0], sacc[a][8 * h + 1]),
+                                       E::pack(sacc[a][8 * h + 2], sacc[a][8 * h + 3]),
+                                       E::pack(sacc[a][8 * h + 4], sacc[a][8 * h + 5]),
+                                       E::pack(sacc[a][8 * h + 6], sacc[a][8 * h + 7])};
+        }
+    };
+
+    // O^T += V^T P^T for block x (V buffer x & 1): two transposed reads of V
+    // rows 32a + 16h + 4g + e and +8 per A operand.
+    auto pv = [&](int x, const u32x4 (&pop)[4]) {
+        const char *vb = lds + v_lane + (x & 1) * LDS::kV;
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt)
-                    oacc[dt] = E::mma(*(const u32x4 *)(vt + (32 * dt + r) * VTS + kc), pop, oacc[dt]);
+        for (int st = 0; st < 4; ++st) {
+            const char *vrp = vb + 16 * st * 16;  // keys 16 st: 16 rows of 16 bytes
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const char *cp = vrp + 4 * dt * VCST;  // 32 columns = 4 chunk columns
+                const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)cp);
+                const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(cp + 8 * 16));
+                const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+                oacc[dt] = E::mma(u32x4{l2[0], l2[1], h2[0], h2[1]}, pop[st], oacc[dt]);
             }
         }
-        __builtin_amdgcn_sched_barrier(0);
-        if (more) store_block(kb + kLongBKV, bf ^ 1);
+    };
+
+    f32x16 sA[2], sB[2];
+    qk(0, sA);
+    wait_dma();
+    __syncthreads();
+
+    // One iteration j: loads for later blocks, phase A, phase B, barrier.
+    // `cur` holds S(j); `nxt` receives S(j+1).  The steady-state variant
+    // (P = parity of j) may assume blocks j..j+DIST exist and are full, and
+    // keeps phases A and B in one basic block so that the compiler can overlap
+    // the MFMAs with the softmax and rotation work; the generic variant checks.
+    auto iteration_steady = [&](auto par_tag, int j, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+        constexpr int P = decltype(par_tag)::value;
+        u32x4 pop[4];
+        smax(cur, kLongBKV);
+        constexpr int RB2 = RAWBUFS == 2 ? P : 0;  // raw buffer of block j + 2
+#pragma unroll
+        for (int m = 0; m < MFULL; ++m) job_steady(m, P);
+        if constexpr (RAWBUFS == 1 && MPER > MFULL) {
+            // one raw buffer: every load of the iteration precedes the mid barrier
+            if (has_job(MFULL)) job_steady(MFULL, P);
+        }
+        qk(j + 1, nxt);
+        sexp(cur, pop);
+        if constexpr (RAWBUFS == 1) {
+            wait_dma();
+            __syncthreads();
+        }
+        pv(j, pop);
+        rotate_one(RB2, P, w);
+        if constexpr (RAWBUFS == 2 && MPER > MFULL) {
+            if (has_job(MFULL)) job_steady(MFULL, P);
+        }
+        rotate_rest(RB2, P);
+        wait_dma();
         __syncthreads();
+    };
+    auto iteration_generic = [&](int j, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+        dma_iter(j);
+        u32x4 pop[4];
+        smax(cur, min(kLongBKV, L - kLongBKV * j));
+        if (j + 1 < nblk) qk(j + 1, nxt);
+        sexp(cur, pop);
+        if constexpr (RAWBUFS == 1) {
+            wait_dma();
+            __syncthreads();
+        }
+        pv(j, pop);
+        if (j + 2 < nblk) rotate((j + 2) % RAWBUFS, j & 1);
+        wait_dma();
+        __syncthreads();
+    };
+    typedef std::integral_constant<int, 0> Even;
+    typedef std::integral_constant<int, 1> Odd;
+
+    // Steady iterations j need blocks up to j + DIST to exist and be full:
+    // j + DIST < nblk - 1, i.e. j < nblk - DIST - 1; taken in pairs.
+    int j = 0;
+    if (nblk - DIST - 1 >= 2) {
+#pragma unroll
+        for (int m = 0; m < MPER; ++m) {
+            const Job jb = job_desc(m);
+            jstep[m] = kLongBKV * jb.rows;
+            jptr[m] = jb.base + (int64_t)(jb.raw ? DIST : 1) * jstep[m];
+            jvoff[m] = (uint32_t)lane * jb.rows;
+#pragma unroll
+            for (int P = 0; P < 2; ++P)
+                jdst[m][P] = jb.lds0 + (jb.raw ? (uint32_t)((P + DIST) % RAWBUFS) : (uint32_t)((P + 1) & 1)) * jb.bufstep;
+        }
+        for (; j + 1 < nblk - DIST - 1; j += 2) {
+            iteration_steady(Even{}, j, sA, sB);
+            iteration_steady(Odd{}, j + 1, sB, sA);
+        }
+    }
+    for (; j < nblk; j += 2) {
+        iteration_generic(j, sA, sB);
+        if (j + 1 < nblk) iteration_generic(j + 1, sB, sA);
     }
 
     if constexpr (ONES) {
-        // O^T row D (the ones row) is in element 4*((D % 32) / 8) of the last
-        // d tile, held by the g = 0 lanes.
+        // O^T row D (the ones column of V) is in element 4*((D % 32) / 8) of
+        // the last d tile, held by the g = 0 lanes.
         constexpr int jl = 4 * ((D - 32 * (NDT - 1)) / 8);
         const float lv = oacc[NDT - 1][jl];
         const float lo = xchg32(lv);
@@ -960,11 +1126,24 @@ struct Choice {
     char name[64];
 };
 
+// The long kernel stages table rows as whole 16-byte chunks; 16-bit tables
+// whose rows are not (head_dim 72 at width head_dim/2) have no long kernel.
+template <int D, int RD, bool FULL> constexpr bool long_ok() {
+    return (FULL ? D : D / 2) * (RD == FRA_DTYPE_F32 ? 4 : 2) % 16 == 0;
+}
+
 template <int D, class E, int RD, bool FULL> void pick_full(bool window, Choice &c) {
+    c.fn = nullptr;
     if constexpr (D <= kWindowMaxD) {
-        c.fn = window ? (KernelFn)window_kernel<D, E, RD, FULL> : (KernelFn)long_kernel<D, E, RD, FULL>;
-    } else {
+        if (window) {
+            c.fn = (KernelFn)window_kernel<D, E, RD, FULL>;
+            c.lds = WinLds<D, FULL>::kBytes;
+            return;
+        }
+    }
+    if constexpr (long_ok<D, RD, FULL>()) {
         c.fn = (KernelFn)long_kernel<D, E, RD, FULL>;
+        c.lds = LongLds<D, RD, FULL>::kBytes;
     }
 }
 
@@ -982,11 +1161,6 @@ template <int D> bool pick_d(bool window, bool full, int qkv, int rd, Choice &c)
         if (rd == FRA_DTYPE_F32) pick_rd<D, F16, FRA_DTYPE_F32>(window, full, c);
         else if (rd == FRA_DTYPE_BF16) pick_rd<D, F16, FRA_DTYPE_BF16>(window, full, c);
         else pick_rd<D, F16, FRA_DTYPE_F16>(window, full, c);
-    }
-    if (window) {
-        c.lds = full ? WinLds<D, true>::kBytes : WinLds<D, false>::kBytes;
-    } else {
-        c.lds = LongLds<D>::kBytes;
     }
     return true;
 }
@@ -1049,6 +1223,26 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
     memset(&c, 0, sizeof(c));
     if (!pick_kernel(d, window, a->rope_width == d, a->qkv_dtype, a->rope_dtype, c))
         return fail(FRA_EUNSUPPORTED, "head_dim=%d has no compiled kernel (built: 64, 72, 80, 96, 128)", d);
+    if (!c.fn)
+        return fail(FRA_EUNSUPPORTED,
+                    "%s cos/sin of width %d (rows of %d bytes) cannot be staged by the long kernel, which "
+                    "moves table rows in 16-byte chunks; pass float32 tables",
+                    dtype_name(a->rope_dtype), a->rope_width, 2 * a->rope_width);
+    if (!window) {
+        // The long kernel moves K, V and table rows from HBM to LDS in 16-byte
+        // chunks, addressing 64 rows of each with 32-bit offsets.
+        if (!small_rows)
+            return fail(FRA_EUNSUPPORTED, "64 rows of q/k/v/out/cos/sin must span less than 2 GiB");
+        const int re = a->rope_dtype == FRA_DTYPE_F32 ? 4 : 2;
+        if (!aligned(a->k, 16) || a->k_stride_seq % 8 || a->k_stride_head % 8)
+            return fail(FRA_EUNSUPPORTED,
+                        "k must be 16-byte aligned with strides that are multiples of 8 elements "
+                        "(segments longer than 64 tokens)");
+        if (!aligned(a->cos, 16) || !aligned(a->sin, 16) || (a->rope_stride_seq * re) % 16)
+            return fail(FRA_EUNSUPPORTED,
+                        "cos/sin must be 16-byte aligned with a row stride that is a multiple of 16 bytes "
+                        "(segments longer than 64 tokens)");
+    }
 
     // Alignment: Q/K/out are read/written in 8-byte quads, V in 16-byte
     // chunks, fp32 tables in 16-byte quads and 16-bit tables in 8-byte quads.

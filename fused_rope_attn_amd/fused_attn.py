@@ -189,31 +189,48 @@ def _validate(q, k, v, cos, sin, cu_seqlens, out) -> None:
             raise ValueError(f"{name} must be on {q.device}, got {t.device}")
 
 
-def _prepare(q, k, v, cos, sin, cu_seqlens):
+def _uses_long_kernel(max_seqlen: int, head_dim: int) -> bool:
+    """The library's kernel choice: segments of at most 64 tokens at
+    head_dim <= 96 go to the window kernel, everything else to the long one."""
+    return not (max_seqlen <= 64 and head_dim <= 96)
+
+
+def _prepare_cu(cu_seqlens, device):
+    cu = cu_seqlens
+    if cu.dtype != torch.int32 or cu.device != device or not cu.is_contiguous():
+        cu = cu.to(device=device, dtype=torch.int32).contiguous()
+    return cu
+
+
+def _prepare(q, k, v, cos, sin, long_kernel: bool):
     """Kernel-readable views: strided q/k/v are used in place when their
     last dim is contiguous and aligned (packed qkv views from a fused qkv
     projection qualify); anything else is copied, as the reference copies
-    non-contiguous inputs (fused_attn.py:187-193)."""
+    non-contiguous inputs (fused_attn.py:187-193).  The long kernel moves K,
+    V and table rows in 16-byte chunks: K must then be 16-byte aligned and
+    table rows whole chunks (16-bit tables whose rows are not, e.g. head_dim
+    72 at width 36, are widened to float32, which is exact)."""
     q = _kernel_layout(q, 8, 4)
-    k = _kernel_layout(k, 8, 4)
+    k = _kernel_layout(k, 16, 8) if long_kernel else _kernel_layout(k, 8, 4)
     v = _kernel_layout(v, 16, 8)
     if cos.dtype != sin.dtype:
         # One table dtype per call: widening bf16/f16 to fp32 is exact.
         cos, sin = cos.float(), sin.float()
-    ra = 16 if cos.dtype == torch.float32 else 8
-    if not (_fits(cos, ra, 4) and _fits(sin, ra, 4) and cos.stride(0) == sin.stride(0)):
+    if long_kernel and (cos.shape[1] * cos.element_size()) % 16:
+        cos, sin = cos.float(), sin.float()
+    ra = 16 if (cos.dtype == torch.float32 or long_kernel) else 8
+    sm = 16 // cos.element_size() if long_kernel else 4
+    if not (_fits(cos, ra, sm) and _fits(sin, ra, sm) and cos.stride(0) == sin.stride(0)):
         cos, sin = cos.contiguous(), sin.contiguous()
-    cu = cu_seqlens
-    if cu.dtype != torch.int32 or cu.device != q.device or not cu.is_contiguous():
-        cu = cu.to(device=q.device, dtype=torch.int32).contiguous()
-    return q, k, v, cos, sin, cu
+    return q, k, v, cos, sin
 
 
 def plan(q, k, v, cos, sin, cu_seqlens, max_seqlen: int, softmax_scale=None) -> dict:
     """Which kernel ``fused_rope_attention`` launches for these inputs
     (no launch): ``{"kernel", "name", "grid", "block", "block_q",
     "block_kv", "lds_bytes"}``."""
-    q2, k2, v2, cos2, sin2, cu = _prepare(q, k, v, cos, sin, cu_seqlens)
+    cu = _prepare_cu(cu_seqlens, q.device)
+    q2, k2, v2, cos2, sin2 = _prepare(q, k, v, cos, sin, _uses_long_kernel(int(max_seqlen), q.shape[2]))
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     scale = q.shape[2] ** -0.5 if softmax_scale is None else softmax_scale
     a = _build_args(q2, k2, v2, cos2, sin2, out, cu, max_seqlen, scale)
@@ -258,17 +275,18 @@ def fused_rope_attention(
     Returns ``out``.
     """
     _validate(q, k, v, cos, sin, cu_seqlens, out)
-    qk, kk, vk, cosk, sink, cu = _prepare(q, k, v, cos, sin, cu_seqlens)
+    cu = _prepare_cu(cu_seqlens, q.device)
 
     if out is None:
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    dst = out if _fits(out, 8, 4) else torch.empty(q.shape, dtype=q.dtype, device=q.device)
 
     if max_seqlen is None:
         max_seqlen = int((cu[1:] - cu[:-1]).max().item())
     max_seqlen = int(max_seqlen)
     if max_seqlen <= 0 or q.shape[0] == 0:
         return out.zero_()
+    qk, kk, vk, cosk, sink = _prepare(q, k, v, cos, sin, _uses_long_kernel(max_seqlen, q.shape[2]))
+    dst = out if _fits(out, 8, 4) else torch.empty(q.shape, dtype=q.dtype, device=q.device)
     scale = q.shape[2] ** -0.5 if softmax_scale is None else float(softmax_scale)
 
     lib = _lib.load()

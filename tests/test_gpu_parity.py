@@ -113,6 +113,22 @@ def test_long_kernel_ragged(device, d, li):
     assert_close(out, oracle(case, "bf16"), EMU_MAX_ABS, EMU_MEAN_ABS, f"long d={d} lens={lens} (emulated)")
 
 
+@pytest.mark.parametrize("d", [72, 80, 96, 128])
+@pytest.mark.parametrize("rope_dtype", [torch.float32, torch.bfloat16])
+def test_long_kernel_full_width_tables(device, d, rope_dtype):
+    # width-head_dim tables: the long kernel stages twice the table bytes (one
+    # raw buffer instead of two at d >= 96 with float32 tables); bf16 tables of
+    # rows that are not whole 16-byte chunks are widened to float32 by the op.
+    lens = [700, 63, 0, 129]
+    case = random_case(lens, h=2, d=d, seed=250 + d, rope_dtype=rope_dtype, width=d)
+    out = f32(run_gpu(case, device))
+    assert_close(out, oracle(case), MAX_ABS, MEAN_ABS, f"long d={d} full-width {rope_dtype}")
+    assert_close(out, oracle(case, "bf16"), EMU_MAX_ABS, EMU_MEAN_ABS, f"long d={d} full-width {rope_dtype} (emulated)")
+    half = dict(case, cos=case["cos"][:, : d // 2].contiguous(), sin=case["sin"][:, : d // 2].contiguous())
+    out_h = f32(run_gpu(half, device))
+    assert_close(out_h, oracle(half), MAX_ABS, MEAN_ABS, f"long d={d} half-width {rope_dtype}")
+
+
 def test_long_kernel_serves_short_segments(device):
     # max_seqlen above 64 routes every segment, short ones too, to the long kernel
     lens = [64, 5, 64, 17]
