@@ -24,7 +24,7 @@ FRA_KERNEL_NONE = 0
 FRA_KERNEL_WINDOW = 1
 FRA_KERNEL_LONG = 2
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class FwdArgs(ctypes.Structure):
@@ -57,6 +57,8 @@ class FwdArgs(ctypes.Structure):
         ("rope_dtype", ctypes.c_int32),
         ("softmax_scale", ctypes.c_float),
         ("flags", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_int64),
     ]
 
 
@@ -70,6 +72,8 @@ class Plan(ctypes.Structure):
         ("block_q", ctypes.c_int32),
         ("block_kv", ctypes.c_int32),
         ("lds_bytes", ctypes.c_int32),
+        ("split_units", ctypes.c_int32),
+        ("split_parts", ctypes.c_int32),
         ("name", ctypes.c_char * 64),
     ]
 
@@ -78,6 +82,7 @@ class Plan(ctypes.Structure):
 SIGNATURES = {
     "fra_fwd_varlen": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.c_void_p]),
     "fra_query_plan": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(Plan)]),
+    "fra_workspace_bytes": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(ctypes.c_int64)]),
     "fra_supports_head_dim": (ctypes.c_int, [ctypes.c_int32]),
     "fra_last_error": (ctypes.c_char_p, []),
     "fra_version": (ctypes.c_char_p, []),

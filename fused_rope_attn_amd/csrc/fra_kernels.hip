@@ -60,6 +60,11 @@ struct KParams {
     int64_t sq_s, sq_h, sk_s, sk_h, sv_s, sv_h, so_s, so_h, sr_s;
     int32_t total, num_heads, num_seqs, max_seqlen;
     int32_t qblocks;      // long kernel: query blocks per (segment, head)
+    // Long kernel, split last round: units (segment, head, query block) from
+    // tail_first on are split into tail_split parts of their key range; the
+    // parts' partial results go to ws (counters, then partials).
+    int32_t tail_first, tail_split;
+    char *ws;
     float scale_log2;     // softmax_scale * log2(e)
 };
 
@@ -665,6 +670,83 @@ template <int D, int RD, bool FULL> struct LongLds {
     static_assert(W * RB % 16 == 0, "table rows must be whole 16-byte chunks");
 };
 
+// ---- split last round: partial results and their merge ------------------------
+//
+// Workspace: per (split unit, part), 256 rows of split_row_floats(D) floats:
+// O (unnormalised, head_dim values), m (running max in scale*log2e units) and
+// l (row sum of P).  split_merge_kernel, launched after the long kernel on
+// the same stream, merges the parts of each unit into the output.
+constexpr int kSplitMaxParts = 8;
+
+__host__ __device__ constexpr int split_row_floats(int d) { return (d + 2 + 3) / 4 * 4; }  // 16-byte pitch
+
+inline int64_t split_workspace_bytes(int64_t units, int parts, int d) {
+    return units * parts * kLongBQ * (int64_t)split_row_floats(d) * 4;
+}
+
+// This workgroup's partial rows (one per lane row q < L).
+template <int D>
+__device__ __forceinline__ void split_write_partial(const KParams &p, int u, int part, int nparts, int q, int L,
+                                                    int w, int r, int g, float m_i, float l_i,
+                                                    const f32x16 (&oacc)[(D + 31) / 32]) {
+    constexpr int NDT = (D + 31) / 32;
+    constexpr int RF = split_row_floats(D);
+    if (q >= L) return;
+    float *row = (float *)p.ws + ((int64_t)((u - p.tail_first) * nparts + part) * kLongBQ + 32 * w + r) * RF;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+            const int d0 = 32 * dt + 8 * jq + 4 * g;
+            if (d0 < D)
+                *(f32x4 *)(row + d0) = f32x4{oacc[dt][4 * jq + 0], oacc[dt][4 * jq + 1], oacc[dt][4 * jq + 2],
+                                             oacc[dt][4 * jq + 3]};
+        }
+    }
+    if (g == 0) {
+        typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
+        *(f32x2 *)(row + D) = f32x2{m_i, l_i};
+    }
+}
+
+// One workgroup per split unit: O = sum_p 2^(m_p - m) O_p / sum_p 2^(m_p - m) l_p
+// with m = max_p m_p, rounded to the output dtype.  Thread items are
+// (row, 4-column chunk), consecutive threads on consecutive chunks.
+template <int D, class E>
+__global__ __launch_bounds__(256) void split_merge_kernel(const KParams p) {
+    constexpr int RF = split_row_floats(D);
+    constexpr int NC = D / 4;
+    const int tu = blockIdx.x, u = p.tail_first + tu, nparts = p.tail_split;
+    const int sh = u / p.qblocks, qblk = u - sh * p.qblocks;
+    const int seg = sh / p.num_heads, head = sh - seg * p.num_heads;
+    int s0 = p.cu[seg], s1 = p.cu[seg + 1];
+    s0 = min(max(s0, 0), p.total);
+    s1 = min(max(s1, 0), p.total);
+    const int L = s1 - s0;
+    if (L <= 0 || qblk * kLongBQ >= L) return;  // uniform: the unit has no rows
+    const float *base = (const float *)p.ws + (int64_t)tu * nparts * kLongBQ * RF;
+    for (int it = threadIdx.x; it < kLongBQ * NC; it += blockDim.x) {
+        const int row = it / NC, c = it - row * NC;
+        const int q = qblk * kLongBQ + row;
+        if (q >= L) continue;
+        float mx = kNegInf;
+        for (int pp = 0; pp < nparts; ++pp) mx = fmaxf(mx, base[(pp * kLongBQ + row) * RF + D]);
+        float l = 0.f;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int pp = 0; pp < nparts; ++pp) {
+            const float *pr = base + (pp * kLongBQ + row) * RF;
+            const float mp = pr[D];
+            if (mp == kNegInf) continue;  // a part with no keys
+            const float wt = __builtin_amdgcn_exp2f(mp - mx);
+            l += wt * pr[D + 1];
+            acc += wt * *(const f32x4 *)(pr + 4 * c);
+        }
+        const float inv = 1.0f / l;
+        char *orow = p.out + ((int64_t)(s0 + q) * p.so_s + (int64_t)head * p.so_h) * 2;
+        *(u32x2 *)(orow + 8 * c) = u32x2{E::pack(acc[0] * inv, acc[1] * inv), E::pack(acc[2] * inv, acc[3] * inv)};
+    }
+}
+
 template <int D, class E, int RD, bool FULL>
 __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) {
     using LDS = LongLds<D, RD, FULL>;
@@ -690,7 +772,17 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     typedef __attribute__((address_space(1))) void glb_void;
     __shared__ __attribute__((aligned(16))) char lds[LDS::kBytes];
 
-    const int u = xcd_remap(blockIdx.x, gridDim.x);
+    // Unit u = (segment, head, query block); workgroups past tail_first take
+    // part `part` of the key range of a unit of the split last round.
+    int u, part = 0, nparts = 1;
+    if ((int)blockIdx.x < p.tail_first) {
+        u = xcd_remap(blockIdx.x, p.tail_first);
+    } else {
+        const int t = xcd_remap(blockIdx.x - p.tail_first, gridDim.x - p.tail_first);
+        nparts = p.tail_split;
+        u = p.tail_first + t / nparts;
+        part = t - (t / nparts) * nparts;
+    }
     const int sh = u / p.qblocks, qblk = u - sh * p.qblocks;
     const int seg = sh / p.num_heads, head = sh - seg * p.num_heads;
     int s0 = p.cu[seg], s1 = p.cu[seg + 1];
@@ -702,13 +794,26 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int r = lane & 31, g = lane >> 5;
-    const int nblk = (L + kLongBKV - 1) / kLongBKV;
+    // Key blocks [b0, b1) of the segment are this workgroup's (all of them
+    // unless the unit is split); Lkv keys, possibly none.
+    const int nblk_all = (L + kLongBKV - 1) / kLongBKV;
+    const int b0 = part * nblk_all / nparts, b1 = (part + 1) * nblk_all / nparts;
+    const int Lkv = min(L, kLongBKV * b1) - kLongBKV * b0;
+    const int nblk = (Lkv + kLongBKV - 1) / kLongBKV;
 
-    const char *kbase = p.k + ((int64_t)s0 * p.sk_s + (int64_t)head * p.sk_h) * 2;
-    const char *vbase = p.v + ((int64_t)s0 * p.sv_s + (int64_t)head * p.sv_h) * 2;
-    const char *cbase = p.cos + (int64_t)s0 * p.sr_s * RB;
-    const char *sbase = p.sin + (int64_t)s0 * p.sr_s * RB;
+    const int64_t k0 = (int64_t)s0 + (int64_t)kLongBKV * b0;  // first key row
+    const char *kbase = p.k + (k0 * p.sk_s + (int64_t)head * p.sk_h) * 2;
+    const char *vbase = p.v + (k0 * p.sv_s + (int64_t)head * p.sv_h) * 2;
+    const char *cbase = p.cos + k0 * p.sr_s * RB;
+    const char *sbase = p.sin + k0 * p.sr_s * RB;
     const int64_t krs = p.sk_s * 2, vrs = p.sv_s * 2, trs = p.sr_s * RB;
+
+    const float sl = p.scale_log2;
+    float m_i = kNegInf, l_i = 0.f;  // running max (scale*log2e units) and row sum
+    f32x16 oacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = f32x16{};
+    if (Lkv > 0) {  // uniform; a part of a split unit may have no keys
 
     // V padding columns [D, 32*NDT) of both buffers: zero, column D ones.
     // They are never overwritten by the staging loads.
@@ -771,7 +876,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         const Job jb = job_desc(m);
         const int x = jb.raw ? xr : xv, bf = jb.raw ? br : bv;
         if (x >= nblk) return;
-        const int nkv = min(kLongBKV, L - kLongBKV * x);
+        const int nkv = min(kLongBKV, Lkv - kLongBKV * x);
         const uint32_t voff = (uint32_t)min(lane, nkv - 1) * jb.rows;
         const char *src = jb.base + (int64_t)x * kLongBKV * jb.rows;
         __builtin_amdgcn_global_load_lds((glb_void *)(src + voff), (lds_void *)(lds + jb.lds0 + bf * jb.bufstep),
@@ -898,11 +1003,6 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     const uint32_t v_lane =
         (uint32_t)(LDS::kOffV + (vcol >> 3) * VCST + (4 * g + ((lane >> 2) & 3)) * 16 + (vcol & 7) * 2);
 
-    const float sl = p.scale_log2;
-    float m_i = kNegInf, l_i = 0.f;
-    f32x16 oacc[NDT];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = f32x16{};
 
     // S^T of block x (K_rot buffer x & 1).
     auto qk = [&](int x, f32x16 (&sacc)[2]) {
@@ -1035,7 +1135,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     auto iteration_generic = [&](int j, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
         dma_iter(j);
         u32x4 pop[4];
-        smax(cur, min(kLongBKV, L - kLongBKV * j));
+        smax(cur, min(kLongBKV, Lkv - kLongBKV * j));
         if (j + 1 < nblk) qk(j + 1, nxt);
         sexp(cur, pop);
         if constexpr (RAWBUFS == 1) {
@@ -1074,6 +1174,8 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         if (j + 1 < nblk) iteration_generic(j + 1, sB, sA);
     }
 
+    }  // Lkv > 0
+
     if constexpr (ONES) {
         // O^T row D (the ones column of V) is in element 4*((D % 32) / 8) of
         // the last d tile, held by the g = 0 lanes.
@@ -1083,6 +1185,10 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         l_i = g ? lo : lv;
     }
     const int q = qblk * kLongBQ + 32 * w + r;
+    if (nparts > 1) {
+        split_write_partial<D>(p, u, part, nparts, q, L, w, r, g, m_i, l_i, oacc);
+        return;
+    }
     if (q < L) {
         const float inv = 1.0f / l_i;
         char *orow = p.out + ((int64_t)(s0 + q) * p.so_s + (int64_t)head * p.so_h) * 2;
@@ -1122,9 +1228,55 @@ constexpr int kWindowMaxD = 96;
 
 struct Choice {
     KernelFn fn;
-    int kernel, grid, block, block_q, block_kv, lds;
+    KernelFn merge;  // split_merge_kernel of the long kernel's instance
+    int kernel, grid, block, block_q, block_kv, lds, split_units, split_parts;
     char name[64];
 };
+
+// Compute units of the current device (cached per device; 256 when no device
+// can be queried, e.g. planning on a host without a GPU).
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            (void)hipGetLastError();
+            n = 256;
+        }
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// The long kernel's split last round.  Units (segment, head, query block)
+// run one workgroup per CU; when the last round of workgroups leaves CUs
+// idle, its units are split into up to kSplitMaxParts parts of their key
+// range (at least two key blocks each on the longest segment), merged by the
+// last part to finish.
+struct SplitPlan {
+    int64_t units;  // units split (the last round)
+    int parts;      // parts per unit (1: no split)
+    int64_t bytes;
+};
+SplitPlan split_plan(int64_t units, int max_seqlen, int d) {
+    SplitPlan sp = {0, 1, 0};
+    const int64_t slots = device_cus();
+    if (units <= 0) return sp;
+    const int64_t rounds = (units + slots - 1) / slots;
+    const int64_t tail = units - (rounds - 1) * slots;
+    int parts = (int)std::min<int64_t>(slots / tail, kSplitMaxParts);
+    parts = std::min(parts, ((max_seqlen + kLongBKV - 1) / kLongBKV) / 2);
+    if (parts < 2) return sp;
+    sp.units = tail;
+    sp.parts = parts;
+    sp.bytes = split_workspace_bytes(tail, parts, d);
+    return sp;
+}
 
 // The long kernel stages table rows as whole 16-byte chunks; 16-bit tables
 // whose rows are not (head_dim 72 at width head_dim/2) have no long kernel.
@@ -1143,6 +1295,7 @@ template <int D, class E, int RD, bool FULL> void pick_full(bool window, Choice 
     }
     if constexpr (long_ok<D, RD, FULL>()) {
         c.fn = (KernelFn)long_kernel<D, E, RD, FULL>;
+        c.merge = (KernelFn)split_merge_kernel<D, E>;
         c.lds = LongLds<D, RD, FULL>::kBytes;
     }
 }
@@ -1280,6 +1433,9 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
 
     const int64_t sh = (int64_t)a->num_seqs * a->num_heads;
     int64_t grid;
+    kp.tail_first = 0;
+    kp.tail_split = 1;
+    kp.ws = nullptr;
     if (window) {
         kp.qblocks = 1;
         grid = (int64_t)a->num_seqs * ((a->num_heads + kWinHeads - 1) / kWinHeads);
@@ -1291,7 +1447,19 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
                  dtype_name(a->rope_dtype));
     } else {
         kp.qblocks = (a->max_seqlen + kLongBQ - 1) / kLongBQ;
-        grid = sh * kp.qblocks;
+        const int64_t units = sh * kp.qblocks;
+        const SplitPlan sp = split_plan(units, a->max_seqlen, d);
+        kp.tail_first = (int32_t)std::min<int64_t>(units, 0x7fffffff);
+        kp.tail_split = 1;
+        kp.ws = (char *)a->workspace;
+        grid = units;
+        if (sp.parts > 1 && a->workspace_bytes >= sp.bytes) {
+            kp.tail_first = (int32_t)(units - sp.units);
+            kp.tail_split = sp.parts;
+            grid = kp.tail_first + sp.units * sp.parts;
+            c.split_units = (int)sp.units;
+            c.split_parts = sp.parts;
+        }
         c.kernel = FRA_KERNEL_LONG;
         c.block = kLongThreads;
         c.block_q = kLongBQ;
@@ -1315,9 +1483,35 @@ int fra_fwd_varlen(const fra_fwd_args *args, void *stream) {
     if (rc != FRA_OK) return rc;
     g_err[0] = 0;
     if (args->total_seq == 0) return FRA_OK;
+    if (c.split_parts > 1 && !args->workspace)
+        return fail(FRA_EINVAL, "workspace_bytes is set but workspace is NULL");
     hipLaunchKernelGGL(c.fn, dim3(c.grid), dim3(c.block), 0, (hipStream_t)stream, kp);
-    const hipError_t e = hipGetLastError();
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(FRA_EHIP, "launch of %s failed: %s", c.name, hipGetErrorString(e));
+    if (c.split_parts > 1) {
+        hipLaunchKernelGGL(c.merge, dim3(c.split_units), dim3(256), 0, (hipStream_t)stream, kp);
+        e = hipGetLastError();
+        if (e != hipSuccess) return fail(FRA_EHIP, "launch of the merge of %s failed: %s", c.name, hipGetErrorString(e));
+    }
+    return FRA_OK;
+}
+
+int fra_workspace_bytes(const fra_fwd_args *args, int64_t *bytes) {
+    if (!bytes) return fail(FRA_EINVAL, "bytes is NULL");
+    *bytes = 0;
+    if (!args) return fail(FRA_EINVAL, "args is NULL");
+    fra_fwd_args a = *args;
+    a.workspace = nullptr;
+    a.workspace_bytes = 0;
+    Choice c;
+    KParams kp;
+    const int rc = plan(&a, c, kp);
+    if (rc != FRA_OK) return rc;
+    if (c.kernel == FRA_KERNEL_LONG) {
+        const SplitPlan sp = split_plan((int64_t)a.num_seqs * a.num_heads * kp.qblocks, a.max_seqlen, a.head_dim);
+        if (sp.parts > 1) *bytes = sp.bytes;
+    }
+    g_err[0] = 0;
     return FRA_OK;
 }
 
@@ -1333,6 +1527,8 @@ int fra_query_plan(const fra_fwd_args *args, fra_plan *out) {
     out->block_q = c.block_q;
     out->block_kv = c.block_kv;
     out->lds_bytes = c.lds;
+    out->split_units = c.split_units;
+    out->split_parts = c.split_parts;
     memcpy(out->name, c.name, sizeof(out->name));
     g_err[0] = 0;
     return FRA_OK;

@@ -11,6 +11,7 @@ Drop-in for the reference module ``fused_attn.py``:
   cache, ``:18-30``): the cos/sin tables the op consumes.
 * ``next_pow2`` -- reference ``fused_attn.py:13-15``.
 """
+import ctypes
 from collections import OrderedDict
 
 import torch
@@ -225,6 +226,13 @@ def _prepare(q, k, v, cos, sin, long_kernel: bool):
     return q, k, v, cos, sin
 
 
+def _workspace_bytes(lib, args) -> int:
+    """Bytes of the long kernel's optional workspace (0: no split applies)."""
+    total = ctypes.c_int64(0)
+    _lib.check(lib.fra_workspace_bytes(args, ctypes.byref(total)))
+    return int(total.value)
+
+
 def plan(q, k, v, cos, sin, cu_seqlens, max_seqlen: int, softmax_scale=None) -> dict:
     """Which kernel ``fused_rope_attention`` launches for these inputs
     (no launch): ``{"kernel", "name", "grid", "block", "block_q",
@@ -235,11 +243,13 @@ def plan(q, k, v, cos, sin, cu_seqlens, max_seqlen: int, softmax_scale=None) -> 
     scale = q.shape[2] ** -0.5 if softmax_scale is None else softmax_scale
     a = _build_args(q2, k2, v2, cos2, sin2, out, cu, max_seqlen, scale)
     lib = _lib.load()
+    a.workspace_bytes = _workspace_bytes(lib, a)  # as fused_rope_attention provides it
     pl = _lib.Plan()
     _lib.check(lib.fra_query_plan(a, pl))
     return {"kernel": {_lib.FRA_KERNEL_WINDOW: "window", _lib.FRA_KERNEL_LONG: "long"}.get(pl.kernel, "none"),
             "name": pl.name.decode(), "grid": pl.grid, "block": pl.block, "block_q": pl.block_q,
-            "block_kv": pl.block_kv, "lds_bytes": pl.lds_bytes}
+            "block_kv": pl.block_kv, "lds_bytes": pl.lds_bytes, "workspace_bytes": a.workspace_bytes,
+            "split_units": pl.split_units, "split_parts": pl.split_parts}
 
 
 def fused_rope_attention(
@@ -291,7 +301,16 @@ def fused_rope_attention(
 
     lib = _lib.load()
     args = _build_args(qk, kk, vk, cosk, sink, dst, cu, max_seqlen, scale)
+    ws = None
     with torch.cuda.device(q.device):
+        # The long kernel splits a partly filled last round of workgroups
+        # along the key range when given a workspace (scratch, per call, from
+        # torch's caching allocator: stream-ordered reuse keeps it alive for
+        # the kernels that use it).
+        nbytes = _workspace_bytes(lib, args)
+        if nbytes:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+            args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
         stream = torch.cuda.current_stream(q.device).cuda_stream
         _lib.check(lib.fra_fwd_varlen(args, stream))
     if dst is not out:

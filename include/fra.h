@@ -17,7 +17,9 @@
  *     status code and leaves a message for fra_last_error().
  *   - All work is enqueued on the caller's HIP stream; nothing is
  *     synchronised, nothing is allocated, no global state is mutated, so the
- *     calls are reentrant and capturable into a HIP graph.
+ *     calls are reentrant and capturable into a HIP graph.  Device memory
+ *     beyond the tensors (the long kernel's optional workspace) is passed in
+ *     by the caller.
  *   - Tensors are [total_seq, num_heads, head_dim] with unit stride on
  *     head_dim; the two outer strides are free (packed qkv views work).
  */
@@ -30,7 +32,7 @@
 extern "C" {
 #endif
 
-#define FRA_ABI_VERSION 1
+#define FRA_ABI_VERSION 2
 
 /* Element types. */
 enum fra_dtype {
@@ -85,6 +87,18 @@ typedef struct fra_fwd_args {
     int32_t rope_dtype;         /* FRA_DTYPE_F32, FRA_DTYPE_BF16 or FRA_DTYPE_F16 */
     float softmax_scale;        /* > 0; the reference uses 1/sqrt(head_dim) */
     int32_t flags;              /* reserved, must be 0 */
+    /*
+     * Optional device workspace of the long kernel (no counterpart in the
+     * reference, whose launch takes no scratch memory).  When it holds at
+     * least the bytes fra_workspace_bytes() reports, the units of a partly
+     * filled last round of workgroups are split along the key range and a
+     * second, small kernel on the same stream merges their parts; otherwise
+     * (NULL / 0) nothing is split.  Scratch only: no contents are expected
+     * before the call or kept after it; calls that share a workspace must
+     * not overlap.
+     */
+    void *workspace;
+    int64_t workspace_bytes;
 } fra_fwd_args;
 
 /* What fra_fwd_varlen() would launch for a set of arguments. */
@@ -95,6 +109,8 @@ typedef struct fra_plan {
     int32_t block_q;            /* query rows per workgroup */
     int32_t block_kv;           /* key/value rows per LDS stage */
     int32_t lds_bytes;          /* static LDS per workgroup */
+    int32_t split_units;        /* long kernel: units of the last round split along keys (0: none) */
+    int32_t split_parts;        /* ... into this many parts each */
     char name[64];              /* kernel instance name */
 } fra_plan;
 
@@ -119,8 +135,17 @@ typedef struct fra_plan {
  */
 int fra_fwd_varlen(const fra_fwd_args *args, void *stream);
 
-/* Fill *plan with the kernel choice for args without launching anything. */
+/* Fill *plan with the kernel choice for args without launching anything
+ * (the split fields reflect args->workspace_bytes). */
 int fra_query_plan(const fra_fwd_args *args, fra_plan *plan);
+
+/*
+ * Workspace bytes the long kernel can use for these arguments (their
+ * workspace fields are ignored); 0 when no split applies.  No counterpart in
+ * the reference (its Triton launch allocates nothing); callers that cannot
+ * allocate simply pass no workspace and get the unsplit kernel.
+ */
+int fra_workspace_bytes(const fra_fwd_args *args, int64_t *bytes);
 
 /* 1 if head_dim has a compiled kernel in this build, else 0. */
 int fra_supports_head_dim(int32_t head_dim);

@@ -278,11 +278,62 @@ def test_workload_parity(device, name):
     got = f32(out if heads is None else out[:, heads])
     ref = oracle(case, heads=heads)
     assert_close(got, ref, MAX_ABS, MEAN_ABS, name)
-    # every head: permuting heads of the inputs permutes heads of the output
+    # every head: permuting heads of the inputs permutes heads of the output --
+    # bit for bit, except where the long kernel splits the units of its last
+    # round along the key range (which units those are moves with the heads,
+    # and a split sums the keys in a different order: within 2 bf16 ulps)
     perm = torch.randperm(w.heads, generator=torch.Generator().manual_seed(7))
     pc = dict(case, q=case["q"][:, perm], k=case["k"][:, perm], v=case["v"][:, perm])
     out_p = run_gpu(pc, device)
-    assert torch.equal(out_p, out[:, perm.to(out.device)])
+    want = out[:, perm.to(out.device)]
+    pl = plan(*(case[x].to(device) for x in ("q", "k", "v", "cos", "sin", "cu_seqlens")),
+              max_seqlen=case["max_seqlen"])
+    if pl["split_parts"] > 1:
+        diff = (out_p.float() - want.float()).abs()
+        assert float(diff.max()) <= 2 * 2 ** -8 * float(want.float().abs().max()), name
+    else:
+        assert torch.equal(out_p, want)
+
+
+def _call_abi(case, device, workspace: bool):
+    """fra_fwd_varlen through the C ABI, with or without the long kernel's
+    workspace (without it, no unit is split)."""
+    import ctypes
+
+    from fused_rope_attn_amd import _lib
+    from fused_rope_attn_amd.fused_attn import _build_args, _workspace_bytes
+    args_t = {x: case[x].to(device) for x in ("q", "k", "v", "cos", "sin")}
+    cu = case["cu_seqlens"].to(device=device, dtype=torch.int32)
+    out = torch.full_like(args_t["q"], float("nan"))
+    a = _build_args(args_t["q"], args_t["k"], args_t["v"], args_t["cos"], args_t["sin"], out, cu,
+                    case["max_seqlen"], case["q"].shape[2] ** -0.5)
+    lib = _lib.load()
+    ws = None
+    nbytes = _workspace_bytes(lib, a)
+    if workspace and nbytes:
+        ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=device)  # scratch: any contents
+        a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
+    pl = _lib.Plan()
+    _lib.check(lib.fra_query_plan(a, pl))
+    _lib.check(lib.fra_fwd_varlen(a, ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)))
+    torch.cuda.synchronize()
+    return out, pl
+
+
+@pytest.mark.parametrize("lens,h,d", [([2000], 3, 80), ([700, 1500, 64, 1], 2, 72), ([9216], 16, 80)])
+def test_long_kernel_split_last_round(device, lens, h, d):
+    # the split path (parts of the key range merged in-kernel) against the
+    # unsplit kernel and the oracle
+    case = random_case(lens, h=h, d=d, seed=260 + d)
+    split, pl = _call_abi(case, device, workspace=True)
+    whole, pl0 = _call_abi(case, device, workspace=False)
+    assert pl.split_parts > 1 and pl0.split_parts == 0
+    assert pl.grid == pl0.grid - pl.split_units + pl.split_units * pl.split_parts
+    assert_close(f32(split), f32(whole), 8e-3, 5e-4, f"split vs whole {lens}")
+    heads = [0] if h > 3 else None
+    ref = oracle(case, heads=heads)
+    got = f32(split if heads is None else split[:, heads])
+    assert_close(got, ref, MAX_ABS, MEAN_ABS, f"split {lens}")
 
 
 # ---- known answers (tests/golden/attention_kat.npz, float64 from the definition) ----
