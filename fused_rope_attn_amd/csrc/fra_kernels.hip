@@ -161,20 +161,22 @@ __device__ __forceinline__ u32 perm(u32 hi_src, u32 lo_src, u32 sel) {
 constexpr u32 kSelLo = 0x05040100u;  // {lo16(lo_src), lo16(hi_src)}
 constexpr u32 kSelHi = 0x07060302u;  // {hi16(lo_src), hi16(hi_src)}
 
-// Split-half rotation of one quad pair, in fp32 with separately rounded
-// products (reference fused_attn.py:340-345 and :385-390; the same order of
-// roundings as the unfused torch path), packed to the storage dtype.
+// Split-half rotation of one quad pair in fp32 (reference
+// fused_attn.py:340-345 and :385-390: x0*cos - x1*sin, x0*sin + x1*cos),
+// packed to the storage dtype.  Each output is one product and one FMA, the
+// form FP contraction (on by default in Triton) gives the reference
+// expression; it differs from separately rounded products by at most one
+// fp32 rounding before the result is rounded to 16 bits.
 template <class E>
 __device__ __forceinline__ void rotate_quad(u32x2 x0w, u32x2 x1w, f32x4 c0, f32x4 s0, f32x4 c1, f32x4 s1,
                                             u32x2 &r0w, u32x2 &r1w) {
-#pragma clang fp contract(off)
     const float x0[4] = {E::lo(x0w[0]), E::hi(x0w[0]), E::lo(x0w[1]), E::hi(x0w[1])};
     const float x1[4] = {E::lo(x1w[0]), E::hi(x1w[0]), E::lo(x1w[1]), E::hi(x1w[1])};
     float r0[4], r1[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        r0[i] = x0[i] * c0[i] - x1[i] * s0[i];
-        r1[i] = x0[i] * s1[i] + x1[i] * c1[i];
+        r0[i] = __builtin_fmaf(x0[i], c0[i], -(x1[i] * s0[i]));
+        r1[i] = __builtin_fmaf(x0[i], s1[i], x1[i] * c1[i]);
     }
     r0w = u32x2{E::pack(r0[0], r0[1]), E::pack(r0[2], r0[3])};
     r1w = u32x2{E::pack(r1[0], r1[1]), E::pack(r1[2], r1[3])};
@@ -709,42 +711,56 @@ __device__ __forceinline__ void split_write_partial(const KParams &p, int u, int
     }
 }
 
-// One workgroup per split unit: O = sum_p 2^(m_p - m) O_p / sum_p 2^(m_p - m) l_p
-// with m = max_p m_p, rounded to the output dtype.  Thread items are
-// (row, 4-column chunk), consecutive threads on consecutive chunks.
+// O = sum_p 2^(m_p - m) O_p / sum_p 2^(m_p - m) l_p with m = max_p m_p,
+// rounded to the output dtype.  Items are (row, 4-column chunk) of a split
+// unit, one per thread (consecutive threads on consecutive chunks of a row):
+// workgroup (tu, blk) of the grid split_units x (head_dim / 4) takes items
+// 256 blk .. 256 blk + 255 of unit tu.
 template <int D, class E>
 __global__ __launch_bounds__(256) void split_merge_kernel(const KParams p) {
     constexpr int RF = split_row_floats(D);
     constexpr int NC = D / 4;
-    const int tu = blockIdx.x, u = p.tail_first + tu, nparts = p.tail_split;
+    const int tu = blockIdx.x / NC, blk = blockIdx.x - tu * NC;
+    const int u = p.tail_first + tu, nparts = p.tail_split;
     const int sh = u / p.qblocks, qblk = u - sh * p.qblocks;
     const int seg = sh / p.num_heads, head = sh - seg * p.num_heads;
     int s0 = p.cu[seg], s1 = p.cu[seg + 1];
     s0 = min(max(s0, 0), p.total);
     s1 = min(max(s1, 0), p.total);
     const int L = s1 - s0;
-    if (L <= 0 || qblk * kLongBQ >= L) return;  // uniform: the unit has no rows
-    const float *base = (const float *)p.ws + (int64_t)tu * nparts * kLongBQ * RF;
-    for (int it = threadIdx.x; it < kLongBQ * NC; it += blockDim.x) {
-        const int row = it / NC, c = it - row * NC;
-        const int q = qblk * kLongBQ + row;
-        if (q >= L) continue;
-        float mx = kNegInf;
-        for (int pp = 0; pp < nparts; ++pp) mx = fmaxf(mx, base[(pp * kLongBQ + row) * RF + D]);
-        float l = 0.f;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int pp = 0; pp < nparts; ++pp) {
-            const float *pr = base + (pp * kLongBQ + row) * RF;
-            const float mp = pr[D];
-            if (mp == kNegInf) continue;  // a part with no keys
-            const float wt = __builtin_amdgcn_exp2f(mp - mx);
-            l += wt * pr[D + 1];
-            acc += wt * *(const f32x4 *)(pr + 4 * c);
+    const int it = blk * 256 + threadIdx.x;  // < kLongBQ * NC
+    const int row = it / NC, c = it - row * NC;
+    const int q = qblk * kLongBQ + row;
+    if (L <= 0 || q >= L) return;
+    const float *base = (const float *)p.ws + ((int64_t)tu * nparts * kLongBQ + row) * RF;
+    float mp[kSplitMaxParts], lp[kSplitMaxParts];
+    f32x4 op[kSplitMaxParts];
+#pragma unroll
+    for (int pp = 0; pp < kSplitMaxParts; ++pp) {
+        if (pp < nparts) {
+            const float *pr = base + (int64_t)pp * kLongBQ * RF;
+            mp[pp] = pr[D];
+            lp[pp] = pr[D + 1];
+            op[pp] = *(const f32x4 *)(pr + 4 * c);
         }
-        const float inv = 1.0f / l;
-        char *orow = p.out + ((int64_t)(s0 + q) * p.so_s + (int64_t)head * p.so_h) * 2;
-        *(u32x2 *)(orow + 8 * c) = u32x2{E::pack(acc[0] * inv, acc[1] * inv), E::pack(acc[2] * inv, acc[3] * inv)};
     }
+    float mx = kNegInf;
+#pragma unroll
+    for (int pp = 0; pp < kSplitMaxParts; ++pp)
+        if (pp < nparts) mx = fmaxf(mx, mp[pp]);
+    float l = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int pp = 0; pp < kSplitMaxParts; ++pp) {
+        if (pp < nparts && mp[pp] != kNegInf) {  // a part with no keys adds nothing
+            const float wt = __builtin_amdgcn_exp2f(mp[pp] - mx);
+            l += wt * lp[pp];
+            acc += wt * op[pp];
+        }
+    }
+    const float inv = 1.0f / l;
+    char *orow = p.out + ((int64_t)(s0 + q) * p.so_s + (int64_t)head * p.so_h) * 2;
+    *(u32x2 *)(orow + 8 * c) = u32x2{E::pack(acc[0] * inv, acc[1] * inv), E::pack(acc[2] * inv, acc[3] * inv)};
 }
 
 template <int D, class E, int RD, bool FULL>
@@ -1489,7 +1505,7 @@ int fra_fwd_varlen(const fra_fwd_args *args, void *stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(FRA_EHIP, "launch of %s failed: %s", c.name, hipGetErrorString(e));
     if (c.split_parts > 1) {
-        hipLaunchKernelGGL(c.merge, dim3(c.split_units), dim3(256), 0, (hipStream_t)stream, kp);
+        hipLaunchKernelGGL(c.merge, dim3(c.split_units * (args->head_dim / 4)), dim3(256), 0, (hipStream_t)stream, kp);
         e = hipGetLastError();
         if (e != hipSuccess) return fail(FRA_EHIP, "launch of the merge of %s failed: %s", c.name, hipGetErrorString(e));
     }
