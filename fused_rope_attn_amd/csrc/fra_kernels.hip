@@ -1272,8 +1272,9 @@ int device_cus() {
 // The long kernel's split last round.  Units (segment, head, query block)
 // run one workgroup per CU; when the last round of workgroups leaves CUs
 // idle, its units are split into up to kSplitMaxParts parts of their key
-// range (at least two key blocks each on the longest segment), merged by the
-// last part to finish.
+// range (at least two key blocks each on the longest segment).  Each part
+// writes its unnormalised rows, running max and row sum to the workspace;
+// split_merge_kernel, the next launch on the stream, combines them.
 struct SplitPlan {
     int64_t units;  // units split (the last round)
     int parts;      // parts per unit (1: no split)
