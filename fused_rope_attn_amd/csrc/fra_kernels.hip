@@ -62,9 +62,10 @@ struct KParams {
     int32_t qblocks;      // long kernel: query blocks per (segment, head)
     // Long kernel, split last round: units (segment, head, query block) from
     // tail_first on are split into tail_split parts of their key range; the
-    // parts' partial results go to ws (counters, then partials).
+    // parts' partial results go to ws.
     int32_t tail_first, tail_split;
     char *ws;
+    int32_t dense_heads;  // window kernel: q, k, v and out have head stride == head_dim
     float scale_log2;     // softmax_scale * log2(e)
 };
 
@@ -217,16 +218,26 @@ __device__ __forceinline__ void load_rotate_quad(const char *xrow, const char *c
 // contiguous in a [tokens, heads, head_dim] tensor -- and LDS turns the slab
 // into MFMA operands (and the output back into slab rows).
 //
-//   1. every global load is issued up front: cos/sin rows, Q, K, V slabs;
-//   2. cos/sin -> LDS as fp32 rows; the Q slab -> LDS (whole, or one
-//      32-token half at a time when the LDS budget asks for it), where
-//      wavefront w rotates the quads of head 4*hg + w it feeds (fp32, rounded
-//      to the storage dtype);
-//   3. the same for K;
-//   4. V -> LDS transposed (V^T per head, kv pairs packed in dwords);
-//   5. per 32-query tile: S^T = K_rot Q_rot^T, softmax, O^T = V^T P^T; the
-//      normalised output stays in registers as packed bf16/fp16;
-//   6. the output rows go through LDS (over V^T) and leave as slab rows.
+//   1. the cos/sin rows and the Q and K slabs are loaded into registers up
+//      front;
+//   2. per 32-token half: the half's cos/sin rows -> LDS as fp32 rows, the
+//      half's Q slab rows -> LDS, where wavefront w rotates the quads of head
+//      4*hg + w it feeds (fp32, rounded to the storage dtype); then the same
+//      for K;
+//   3. the V slab goes from HBM straight to LDS (global_load_lds_dwordx4) as
+//      padded rows, over the dead staging buffers;
+//   4. per 32-query tile: S^T = K_rot Q_rot^T, softmax, O^T = V^T P^T with the
+//      V^T operands read by ds_read_b64_tr_b16; the normalised output stays in
+//      registers as packed bf16/fp16;
+//   5. the output rows go through LDS (over V) and leave as slab rows.
+//
+// Nothing but the staging buffers of one half lives in LDS while Q and K are
+// rotated, and V never passes through registers, so at D = 80 a workgroup
+// needs 45 KB of LDS and three fit on a CU: a 144-window, 16-head layer (576
+// workgroups) runs in one round on 256 CUs.
+//
+// Rows past the segment (L < 64) load the segment's first (Q, K) or last (V)
+// row: finite values whose keys are masked and whose queries are not stored.
 //
 // Lane (r, g) (r = lane & 31, g = lane >> 5) of a wavefront holds the
 // operands of tokens r and r + 32: K_rot rows as the A operand of S^T and
@@ -235,57 +246,97 @@ __device__ __forceinline__ void load_rotate_quad(const char *xrow, const char *c
 // free as long as Q and K share it).
 
 constexpr int kWinHeads = 4;     // heads (wavefronts) per workgroup
-constexpr int kWinWaves = 2;     // wavefronts per SIMD the register budget is sized for
 constexpr int kWinThreads = 64 * kWinHeads;
+
+// Bytes of an LDS row of V: at least `need`, a multiple of 64 bytes, and
+// 16 or 48 dwords past a multiple of 64 dwords, so that the four rows one
+// 16-lane group of a transposed read touches fall in disjoint banks.
+constexpr int win_vpitch(int need) {
+    int dw = (need + 63) / 64 * 16;
+    while (dw % 64 != 16 && dw % 64 != 48) dw += 16;
+    return 4 * dw;
+}
+
+// The items first, first + kWinThreads, ... of a row-major [rows][N] grid as
+// (row, col), stepped without divisions: kWinThreads = Q*N + R.
+template <int N> struct GridWalk {
+    static constexpr int Q = kWinThreads / N, R = kWinThreads % N;
+    int row, col;
+    __device__ __forceinline__ explicit GridWalk(int first) : row(first / N), col(first - (first / N) * N) {}
+    // Advances to the next item; true when the column wrapped (one more row).
+    __device__ __forceinline__ bool next() {
+        row += Q;
+        col += R;
+        const bool carry = col >= N;
+        if (carry) {
+            col -= N;
+            ++row;
+        }
+        return carry;
+    }
+};
+template <bool B> struct BoolTag {
+    static constexpr bool value = B;
+};
 
 template <int D, bool FULL> struct WinLds {
     static constexpr int W = FULL ? D : D / 2;         // table width
     static constexpr int CS = 2 * W + 4;               // fp32 per [cos | sin] row, +4 pad (conflict-free b128 reads)
     static constexpr int SLAB = kWinHeads * D * 2;     // bytes of one token's slab
     static constexpr int PITCH = SLAB + 16;            // LDS row pitch of a staged slab (one pad chunk)
-    static constexpr int VTS = 36;                     // dwords per V^T row: 32 kv pairs + 4 pad
-    static constexpr int kTableBytes = 64 * CS * 4;
-    static constexpr int kStageRows = kWinWaves == 2 ? 64 : 32;  // slab rows staged at once
-    static constexpr int kHalfBytes = kStageRows * PITCH;
+    static constexpr int NDT = (D + 31) / 32;          // 32-row tiles of O^T
+    // A V row holds the slab and the columns the last head's padding tile
+    // reads past it (values only reach discarded output rows).
+    static constexpr int VNEED = 2 * ((kWinHeads - 1) * D + 32 * NDT) > SLAB ? 2 * ((kWinHeads - 1) * D + 32 * NDT) : SLAB;
+    static constexpr int VP = win_vpitch(VNEED);
+    static constexpr int VPC = VP / 16;                // 16-byte slots per V row
+    static constexpr int kTableBytes = 32 * CS * 4;    // tables of one 32-token half
+    static constexpr int kHalfBytes = 32 * PITCH;      // Q or K slab rows of one half
     static constexpr int kRotBytes = kTableBytes + kHalfBytes;
-    static constexpr int kVtBytes = kWinHeads * D * VTS * 4;
+    static constexpr int kVBytes = 64 * VP;
     static constexpr int kOutBytes = 64 * PITCH;
-    static constexpr int kMax2 = kVtBytes > kOutBytes ? kVtBytes : kOutBytes;
+    static constexpr int kMax2 = kVBytes > kOutBytes ? kVBytes : kOutBytes;
     static constexpr int kMain = kRotBytes > kMax2 ? kRotBytes : kMax2;
     static constexpr int kBytes = kMain + 16;          // + a 16-byte trash slot
+    // Wavefronts per SIMD the register budget is sized for: three
+    // workgroups per CU when their LDS fits and the loads held in registers
+    // leave room (half-width tables, D = 64 or 80: at most 166 VGPRs without
+    // spills), else two.
+    static constexpr int kWaves = !FULL && D <= 80 && D % 16 == 0 && 3 * kBytes <= 160 * 1024 ? 3 : 2;
 };
 
 template <int D, class E, int RD, bool FULL>
-__global__ __launch_bounds__(kWinThreads, kWinWaves) void window_kernel(const KParams p) {
+__global__ __launch_bounds__(kWinThreads, (WinLds<D, FULL>::kWaves)) void window_kernel(const KParams p) {
     using LDS = WinLds<D, FULL>;
     constexpr int NQ = D / 8;                 // quads per half
     constexpr int S = (NQ + 1) / 2;           // 16-deep k-steps of QK^T
-    constexpr int NDT = (D + 31) / 32;        // 32-row tiles of O^T
-    constexpr int VTS = LDS::VTS;
+    constexpr int NDT = LDS::NDT;
     constexpr int W = LDS::W;
     constexpr int CS = LDS::CS;
     constexpr int PITCH = LDS::PITCH;
+    constexpr int VP = LDS::VP, VPC = LDS::VPC;
     constexpr int HCH = D / 8;                // 16-byte chunks per head row
     constexpr int NCH = kWinHeads * HCH;      // chunks per slab row
+    constexpr int SLABB = LDS::SLAB;          // bytes of one token's slab
+    static_assert(SLABB % 64 == 0, "slab rows are whole 64-byte sectors");
     constexpr int RB = Rope<RD>::kBytes;
     constexpr int TQ = W / 4;                 // table quads per row
-    constexpr int TITEMS = 64 * TQ * 2;       // (token, quad, table)
+    constexpr int TN = 2 * TQ;                // table items per token: cos quads, then sin quads
+    constexpr int TITEMS = 64 * TN;
     constexpr int TPER = (TITEMS + kWinThreads - 1) / kWinThreads;
-    constexpr int SITEMS = 64 * NCH;          // (token, chunk) of a Q/K slab or the output
-    constexpr int SPER = (SITEMS + kWinThreads - 1) / kWinThreads;
-    constexpr int VITEMS = 32 * NCH;          // (token pair, chunk) of the V slab
-    constexpr int VPER = (VITEMS + kWinThreads - 1) / kWinThreads;
-    constexpr int OQ = NDT * 4;               // output quads per lane and query tile
-    // V^T row rho (= head*D + d) stores kv pair j at dword column
-    // j ^ vswz(rho): with the 36-dword pitch this makes both the staging
-    // writes and the operand reads (b64, pairs of columns) 2-way at most
-    // across the 64 banks.  The xor value is even, so column pairs stay
-    // adjacent and 8-byte aligned.
-    auto vswz = [](int rho) { return 2 * ((rho >> 4) & 15); };
+    constexpr int SPER = 64 * NCH / kWinThreads;  // (token, chunk) items of a slab per thread
+    static_assert(64 * NCH % kWinThreads == 0, "slab items divide evenly");
+    // Item k of a slab belongs to half k / (SPER / 2) when a half is a whole
+    // number of item rounds (D != 72); otherwise it is tested per item.
+    constexpr bool KHALF = 32 * NCH % kWinThreads == 0;
+    constexpr int VPER = (VPC + kWinHeads - 1) / kWinHeads;  // V direct loads per wavefront
+    typedef short v4i16 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+    typedef __attribute__((address_space(3))) void lds_void;
+    typedef __attribute__((address_space(1))) void glb_void;
     __shared__ __attribute__((aligned(16))) char lds[LDS::kBytes];
-    float *tab = (float *)lds;                                  // [64][CS] fp32 tables
-    char *half = lds + LDS::kTableBytes;                        // [32][PITCH]: half a Q or K slab
-    u32 *vt_all = (u32 *)lds;                                   // [4][D][VTS] V^T, after the rotations
+    float *tab = (float *)lds;                                  // [32][CS] fp32 tables of one half
+    char *half = lds + LDS::kTableBytes;                        // [32][PITCH]: one half of a Q or K slab
     char *oslab = lds;                                          // [64][PITCH] output rows, after PV
     char *trash = lds + LDS::kMain;                             // sink of out-of-range staging items
 
@@ -311,87 +362,105 @@ __global__ __launch_bounds__(kWinThreads, kWinWaves) void window_kernel(const KP
     const char *vb = p.v + ((int64_t)s0 * p.sv_s + (int64_t)h0 * p.sv_h) * 2;
     const char *cb = p.cos + (int64_t)s0 * p.sr_s * RB;
     const char *sb = p.sin + (int64_t)s0 * p.sr_s * RB;
-    char *ob = p.out + ((int64_t)s0 * p.so_s + (int64_t)h0 * p.so_h) * 2;
-    const uint32_t qrs = (uint32_t)p.sq_s * 2, krs = (uint32_t)p.sk_s * 2, vrs = (uint32_t)p.sv_s * 2;
-    const uint32_t qhs = (uint32_t)p.sq_h * 2, khs = (uint32_t)p.sk_h * 2, vhs = (uint32_t)p.sv_h * 2;
-    const uint32_t ors = (uint32_t)p.so_s * 2, ohs = (uint32_t)p.so_h * 2;
     const uint32_t trs = (uint32_t)p.sr_s * RB;
+    // Full window, four heads, each token's heads adjacent in every tensor:
+    // chunk c of slab row t is at t * row_stride + 16 c, and row offsets are
+    // stepped instead of multiplied.
+    const bool fast = p.dense_heads && nh == kWinHeads && L == 64;  // uniform
+    // Byte offset of chunk `col` of a slab row: head col / HCH (heads past
+    // the group's last read its first), chunk col % HCH.
+    auto chunk_off = [&](int col, uint32_t hs) {
+        const int hh = col / HCH;
+        const uint32_t hd = hh < nh ? (uint32_t)hh : 0u;
+        return hd * hs + (uint32_t)(16 * (col - hh * HCH));
+    };
 
-    // ---- 1. every global load, back to back: tables, Q, K and V slabs ----------
-    // Rows past the segment and chunks of heads past the last one read the
-    // segment's first row / the group's first head; their values are never used.
+    // ---- 1. global loads into registers, back to back: tables, Q and K slabs -------
+    // Q and K are read once and the output is written once: those accesses
+    // are non-temporal, so that they neither evict the cos/sin rows the
+    // window's other head groups share nor leave dirty output lines in L2
+    // for the end of the kernel to write back (measured: 1.6 us of 29 at a
+    // 144-window layer).
     f32x4 tv[TPER];
-    int t1 = fresh(tid);
+    {
+        GridWalk<TN> it(fresh(tid));
 #pragma unroll
-    for (int k = 0; k < TPER; ++k) {
-        const int it = min(t1 + k * kWinThreads, TITEMS - 1);
-        const int tok = it / (2 * TQ), rem = it - tok * 2 * TQ;
-        const int tbl = rem / TQ, qd = rem - tbl * TQ;
-        const uint32_t off = (uint32_t)(tok < L ? tok : 0) * trs + (uint32_t)(4 * qd * RB);
-        tv[k] = Rope<RD>::quad((tbl ? sb : cb) + off);
+        for (int k = 0; k < TPER; ++k) {
+            const int tok = min(it.row, 63), c = it.col;
+            const bool is_sin = c >= TQ;
+            const uint32_t off = (uint32_t)(tok < L ? tok : 0) * trs + (uint32_t)(4 * RB * (is_sin ? c - TQ : c));
+            tv[k] = Rope<RD>::quad((is_sin ? sb : cb) + off);
+            it.next();
+        }
     }
     u32x4 qs[SPER], ks[SPER];
-    t1 = fresh(tid);
+    {
+        const uint32_t qrs = (uint32_t)p.sq_s * 2, krs = (uint32_t)p.sk_s * 2;
+        const uint32_t qhs = (uint32_t)p.sq_h * 2, khs = (uint32_t)p.sk_h * 2;
+        auto load_slabs = [&](auto fast_tag) {
+            constexpr bool F = decltype(fast_tag)::value;
+            GridWalk<NCH> it(fresh(tid));
+            uint32_t qro = (uint32_t)it.row * qrs, kro = (uint32_t)it.row * krs;
 #pragma unroll
-    for (int k = 0; k < SPER; ++k) {
-        const int it = min(t1 + k * kWinThreads, SITEMS - 1);
-        const int tok = it / NCH, wc = it - tok * NCH;
-        const int hh = wc / HCH, c = wc - hh * HCH;
-        const uint32_t row = tok < L ? tok : 0, hd = hh < nh ? hh : 0;
-        qs[k] = *(const u32x4 *)(qb + (row * qrs + hd * qhs + 16 * c));
-        ks[k] = *(const u32x4 *)(kb + (row * krs + hd * khs + 16 * c));
-    }
-    // V rows 2j, 2j+1 of the slab.
-    u32x4 va[VPER], vv[VPER];
-    t1 = fresh(tid);
-#pragma unroll
-    for (int k = 0; k < VPER; ++k) {
-        const int it = min(t1 + k * kWinThreads, VITEMS - 1);
-        const int j = it / NCH, wc = it - j * NCH;
-        const int hh = wc / HCH, c = wc - hh * HCH;
-        const uint32_t ra = 2 * j < L ? 2 * j : 0, rb = 2 * j + 1 < L ? 2 * j + 1 : 0;
-        const uint32_t hd = hh < nh ? hh : 0;
-        va[k] = *(const u32x4 *)(vb + (ra * vrs + hd * vhs + 16 * c));
-        vv[k] = *(const u32x4 *)(vb + (rb * vrs + hd * vhs + 16 * c));
+            for (int k = 0; k < SPER; ++k) {
+                if constexpr (F) {
+                    qs[k] = __builtin_nontemporal_load((const u32x4 *)(qb + (qro + 16 * it.col)));
+                    ks[k] = __builtin_nontemporal_load((const u32x4 *)(kb + (kro + 16 * it.col)));
+                } else {
+                    const uint32_t row = it.row < L ? (uint32_t)it.row : 0u;
+                    qs[k] = __builtin_nontemporal_load((const u32x4 *)(qb + (row * qrs + chunk_off(it.col, qhs))));
+                    ks[k] = __builtin_nontemporal_load((const u32x4 *)(kb + (row * krs + chunk_off(it.col, khs))));
+                }
+                const bool cy = it.next();
+                if constexpr (F) {
+                    qro += GridWalk<NCH>::Q * qrs + (cy ? qrs : 0u);
+                    kro += GridWalk<NCH>::Q * krs + (cy ? krs : 0u);
+                }
+            }
+        };
+        if (fast) load_slabs(BoolTag<true>{});
+        else load_slabs(BoolTag<false>{});
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- 2. tables to LDS; Q staged and rotated ---------------------------------
+    // ---- 2. per half: tables and Q staged and rotated, then K ------------------------
     // Staging writes are branch-free (a branch here would make the compiler
-    // wait for every outstanding load): items out of range go to the trash slot.
-    t1 = fresh(tid);
+    // wait for every outstanding load): items of the other half go to the
+    // trash slot unless the half is known per item at compile time.
+    auto stage_tab = [&](int hf) {
+        GridWalk<TN> it(fresh(tid));
 #pragma unroll
-    for (int k = 0; k < TPER; ++k) {
-        const int it = t1 + k * kWinThreads;
-        const bool in = TITEMS % kWinThreads == 0 || it < TITEMS;
-        const int itc = in ? it : 0;
-        const int tok = itc / (2 * TQ), rem = itc - tok * 2 * TQ;
-        const int tbl = rem / TQ, qd = rem - tbl * TQ;
-        *(f32x4 *)(in ? (char *)(tab + tok * CS + tbl * W + 4 * qd) : trash) = tv[k];
-    }
-    // Writes the items of tokens [R*hf, R*hf + R) of a slab into `half`
-    // (R = kStageRows: all 64 rows at once when LDS allows, else 32).
-    constexpr int R = LDS::kStageRows;
+        for (int k = 0; k < TPER; ++k) {
+            const bool in = (TITEMS % kWinThreads == 0 || it.row < 64) && (it.row >> 5) == hf;
+            const int c = it.col, is_sin = c >= TQ ? 1 : 0;
+            char *dst = (char *)(tab + (it.row - 32 * hf) * CS + is_sin * W + 4 * (c - is_sin * TQ));
+            *(f32x4 *)(in ? dst : trash) = tv[k];
+            it.next();
+        }
+    };
     auto stage_half = [&](const u32x4 (&x)[SPER], int hf) {
-        const int ts = fresh(tid);
+        GridWalk<NCH> it(fresh(tid));
 #pragma unroll
         for (int k = 0; k < SPER; ++k) {
-            const int it = ts + k * kWinThreads;
-            const int tok = it / NCH, wc = it - tok * NCH;
-            const bool in = (SITEMS % kWinThreads == 0 || it < SITEMS) && (R == 64 || (tok >> 5) == hf);
-            *(u32x4 *)(in ? half + (tok - R * hf) * PITCH + 16 * wc : trash) = x[k];
+            char *dst = half + (it.row - 32 * hf) * PITCH + 16 * it.col;
+            if constexpr (KHALF) {
+                if (k / (SPER / 2) == hf) *(u32x4 *)dst = x[k];
+            } else {
+                *(u32x4 *)((it.row >> 5) == hf ? dst : trash) = x[k];
+            }
+            it.next();
         }
     };
     // Rotates this wavefront's quads of the staged half into MFMA operands.
-    auto rotate_half = [&](u32x4 (&op)[S], int hf) {
-        const int tok = r + 32 * hf;
-        const float *crow = tab + tok * CS;
-        const char *xrow = half + (R == 64 ? tok : r) * PITCH + w * (2 * D);
+    // Quad i = g*S + t exists unless NQ is odd and it is the last one.
+    auto rotate_half = [&](u32x4 (&op)[S]) {
+        const float *crow = tab + r * CS;
+        const char *xrow = half + r * PITCH + w * (2 * D);
 #pragma unroll
         for (int t = 0; t < S; ++t) {
+            const bool maybe_pad = t >= NQ - S;   // compile time; true only for odd NQ
             const int i = g * S + t;
-            const bool has = tok < L && i < NQ;
-            const int il = i < NQ ? i : 0;
+            const int il = maybe_pad ? (i < NQ ? i : 0) : i;
             const f32x4 c0 = *(const f32x4 *)(crow + 4 * il);
             const f32x4 s0v = *(const f32x4 *)(crow + W + 4 * il);
             f32x4 c1 = c0, s1v = s0v;
@@ -401,85 +470,85 @@ __global__ __launch_bounds__(kWinThreads, kWinWaves) void window_kernel(const KP
             }
             u32x2 x0 = *(const u32x2 *)(xrow + 8 * il);
             u32x2 x1 = *(const u32x2 *)(xrow + D + 8 * il);
-            if (!has) x0 = x1 = u32x2{0u, 0u};
+            if (maybe_pad && i >= NQ) x0 = x1 = u32x2{0u, 0u};
             u32x2 a0, a1;
             rotate_quad<E>(x0, x1, c0, s0v, c1, s1v, a0, a1);
             op[t] = u32x4{a0[0], a0[1], a1[0], a1[1]};
         }
+        // The packed operands are materialised here: left to itself the
+        // compiler sinks the rotation towards the attention that consumes it
+        // and keeps its fp32 intermediates (twice the registers) alive
+        // across the staging of the next slabs.
+#pragma unroll
+        for (int t = 0; t < S; ++t) asm volatile("" : "+v"(op[t]));
     };
     u32x4 qop[2][S], kop[2][S];
-    if constexpr (R == 64) {
-        stage_half(qs, 0);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+        if (hf == 1 && L <= 32) break;  // uniform: no second half (its operands are never read)
+        stage_tab(hf);
+        stage_half(qs, hf);
         __syncthreads();
-        rotate_half(qop[0], 0);
-        rotate_half(qop[1], 1);
+        rotate_half(qop[hf]);
         __syncthreads();
-        // ---- 3. the K slab -----------------------------------------------------------
-        stage_half(ks, 0);
+        stage_half(ks, hf);
         __syncthreads();
-        rotate_half(kop[0], 0);
-        rotate_half(kop[1], 1);
-    } else {
-        stage_half(qs, 0);
-        __syncthreads();
-        rotate_half(qop[0], 0);
-        __syncthreads();
-        stage_half(qs, 1);
-        __syncthreads();
-        rotate_half(qop[1], 1);
-        __syncthreads();
-        // ---- 3. the K slab -----------------------------------------------------------
-        stage_half(ks, 0);
-        __syncthreads();
-        rotate_half(kop[0], 0);
-        __syncthreads();
-        stage_half(ks, 1);
-        __syncthreads();
-        rotate_half(kop[1], 1);
+        rotate_half(kop[hf]);
+        __syncthreads();  // tables and the staged slab are dead
     }
-    __syncthreads();  // tables and the staged slab are dead: V^T goes over them
 
-    // ---- 4. V^T: vt[hh][d][j] = {V[2j][d], V[2j+1][d]} ------------------------------
-    t1 = fresh(tid);
+    // ---- 3. V rows straight from HBM into LDS ------------------------------------------
+    // Direct load m moves LDS slots 64m .. 64m + 63 (16 bytes each, lane =
+    // slot): slot s is chunk s % VPC of V row s / VPC.  Slots past the slab
+    // are padding and not loaded; rows past the segment load its last row.
+    {
+        const uint32_t vrs = (uint32_t)p.sv_s * 2, vhs = (uint32_t)p.sv_h * 2;
+        auto load_v = [&](auto fast_tag) {
+            constexpr bool F = decltype(fast_tag)::value;
+            GridWalk<VPC> it(fresh(tid));  // slot 64 (w + 4k) + lane
+            uint32_t vro = (uint32_t)it.row * vrs;
 #pragma unroll
-    for (int k = 0; k < VPER; ++k) {
-        const int it = t1 + k * kWinThreads;
-        const bool in = VITEMS % kWinThreads == 0 || it < VITEMS;
-        const int itc = in ? it : 0;
-        const int j = itc / NCH, wc = itc - j * NCH;
-        const int hh = wc / HCH, c = wc - hh * HCH;
-        u32x4 A = va[k], B = vv[k];
-        if (2 * j >= L) A = u32x4{0u, 0u, 0u, 0u};
-        if (2 * j + 1 >= L) B = u32x4{0u, 0u, 0u, 0u};
-        // rho is a multiple of 8, so the item's 8 rows share one swizzle value
-        const int rho = hh * D + 8 * c;
-        u32 *col = vt_all + rho * VTS + (j ^ vswz(rho));
-        const int cs = in ? VTS : 0;  // out-of-range items write the trash slot 8 times
-        if (!in) col = (u32 *)trash;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            col[(2 * e) * cs] = perm(B[e], A[e], kSelLo);
-            col[(2 * e + 1) * cs] = perm(B[e], A[e], kSelHi);
-        }
+            for (int k = 0; k < VPER; ++k) {
+                const int m = w + kWinHeads * k;
+                if (VPC % kWinHeads == 0 || m < VPC) {  // uniform
+                    if (it.col < NCH) {
+                        uint32_t off;
+                        if constexpr (F) off = vro + 16 * it.col;
+                        else off = (uint32_t)min(it.row, L - 1) * vrs + chunk_off(it.col, vhs);
+                        __builtin_amdgcn_global_load_lds((glb_void *)(vb + off), (lds_void *)(lds + 1024 * m), 16, 0, 0);
+                    }
+                }
+                const bool cy = it.next();
+                if constexpr (F) vro += GridWalk<VPC>::Q * vrs + (cy ? vrs : 0u);
+            }
+        };
+        if (fast) load_v(BoolTag<true>{});
+        else load_v(BoolTag<false>{});
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     __syncthreads();
 
-    // ---- 5. attention per 32-query tile ---------------------------------------------
-    // The query-tile loop stays rolled (unrolled, the compiler overlaps the two
-    // tiles and runs out of registers); the tile's operands and results are
-    // selected with explicit selects, as a register array must not be indexed
-    // by the loop variable.
+    // ---- 4. attention per 32-query tile ---------------------------------------------
+    // The two tiles run one after the other (a scheduling barrier between
+    // them keeps the compiler from overlapping them, which would need both
+    // tiles' registers at once); a tile's packed output is kept in registers
+    // until V is dead.
+    //
+    // V^T operands: ds_read_b64_tr_b16 works on groups of 16 lanes; lane
+    // c = 4e + qq of a group addresses the 8 bytes at V[row0 + e][col0 + 4qq],
+    // and lane i of the group receives V[row0 + 0..3][col0 + i].  Group G =
+    // lane >> 4 takes columns 16 (G & 1) of the 32-column tile and rows 4g,
+    // so lane l receives keys 4g .. 4g + 3 of column (l & 31): the A operand
+    // of O^T = V^T P^T for k-slots 0..3, and the read 8 rows further down for
+    // k-slots 4..7.
+    constexpr int OQV = (D / 32) * 4 + (D % 32) / 8;  // quads with d0 < D for g = 0 (D % 8 == 0)
     const float sl = p.scale_log2;
     const int nkt = (L + 31) >> 5;
-    const u32 *vt = vt_all + w * (D * VTS);
-    u32x2 outq[2][OQ];  // packed normalised output quads (q = 32b + r, d0 = 32dt + 8jq + 4g)
-#pragma unroll 1
-    for (int b = 0; b < 2; ++b) {
-        __builtin_amdgcn_sched_barrier(0);
-        if (b * 32 >= L || !active) break;  // uniform within the wavefront; no barrier inside
-        u32x4 qcur[S];
-#pragma unroll
-        for (int t = 0; t < S; ++t) qcur[t] = b ? qop[1][t] : qop[0][t];
+    const uint32_t v_lane =
+        (uint32_t)((4 * g + ((lane >> 2) & 3)) * VP + 2 * (w * D + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
+    // Output quad i of a tile: d0 = 32 (i / 4) + 8 (i % 4) + 4g.  Quads past
+    // OQV (d0 >= D for both g) are not kept; quad OQV - 1 may be half valid.
+    auto tile = [&](const u32x4 (&qcur)[S], u32x2 (&outq)[OQV]) {
         // S^T tiles: rows kv, columns q.  Lane (r, g) holds q = 32b + r and
         // kv = 32a + 8(j/4) + 4g + (j%4) in element j of sacc[a].
         f32x16 sacc[2];
@@ -491,16 +560,25 @@ __global__ __launch_bounds__(kWinThreads, kWinWaves) void window_kernel(const KP
                 for (int t = 0; t < S; ++t) sacc[a] = E::mma(kop[a][t], qcur[t], sacc[a]);
             }
         }
-        float mx = kNegInf;
+        if (L < 64) {  // uniform: keys past the segment
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
+            for (int a = 0; a < 2; ++a) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int kv = 32 * a + 8 * (j >> 2) + 4 * g + (j & 3);
-                if (kv >= L) sacc[a][j] = kNegInf;
-                mx = fmaxf(mx, sacc[a][j]);
+                for (int j = 0; j < 16; ++j) {
+                    const int kv = 32 * a + 8 * (j >> 2) + 4 * g + (j & 3);
+                    if (kv >= L) sacc[a][j] = kNegInf;
+                }
             }
         }
+        float t8[11];
+#pragma unroll
+        for (int k = 0; k < 10; ++k) {
+            const int e = 3 * k;
+            t8[k] = max3f(sacc[e >> 4][e & 15], sacc[(e + 1) >> 4][(e + 1) & 15], sacc[(e + 2) >> 4][(e + 2) & 15]);
+        }
+        t8[10] = fmaxf(sacc[1][14], sacc[1][15]);
+        float mx = fmaxf(max3f(max3f(t8[0], t8[1], t8[2]), max3f(t8[3], t8[4], t8[5]), max3f(t8[6], t8[7], t8[8])),
+                         fmaxf(t8[9], t8[10]));
         mx = fmaxf(mx, xchg32(mx));
         const float mneg = -mx * sl;
         float lsum = 0.f;
@@ -529,70 +607,73 @@ __global__ __launch_bounds__(kWinThreads, kWinWaves) void window_kernel(const KP
                                   E::pack(sacc[a][8 * h + 6], sacc[a][8 * h + 7])};
         }
         // One 32-row d tile of O^T at a time; element j of oacc is
-        // q = 32b + r, d = 32dt + 8(j/4) + 4g + (j%4).
-        u32x2 ocur[OQ];
+        // q = 32b + r, d = 32dt + 8(j/4) + 4g + (j%4).  Rows d >= D read
+        // columns of the next head or row padding; they are never stored.
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
-            const int d = 32 * dt + r;
-            const int dr = min(d, D - 1);
-            const u32 *vrow = vt + dr * VTS;
-            const int xs = vswz(w * D + dr);
             f32x16 oacc = f32x16{};
 #pragma unroll
             for (int a = 0; a < 2; ++a) {
                 if (a >= nkt) break;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    const int kc = 16 * a + 8 * h + 2 * g;  // dword column of kv = 32a + 16h + 4g
-                    const u32x2 lo = *(const u32x2 *)(vrow + (kc ^ xs));
-                    const u32x2 hi = *(const u32x2 *)(vrow + ((kc + 4) ^ xs));
-                    u32x4 vop = {lo[0], lo[1], hi[0], hi[1]};
-                    if (d >= D) vop = u32x4{0u, 0u, 0u, 0u};
-                    oacc = E::mma(vop, pop[a][h], oacc);
+                    const char *cp = lds + v_lane + (32 * a + 16 * h) * VP + 64 * dt;
+                    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)cp);
+                    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(cp + 8 * VP));
+                    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+                    oacc = E::mma(u32x4{l2[0], l2[1], h2[0], h2[1]}, pop[a][h], oacc);
                 }
             }
 #pragma unroll
             for (int jq = 0; jq < 4; ++jq)
-                ocur[4 * dt + jq] = u32x2{E::pack(oacc[4 * jq + 0] * inv, oacc[4 * jq + 1] * inv),
-                                          E::pack(oacc[4 * jq + 2] * inv, oacc[4 * jq + 3] * inv)};
+                if (4 * dt + jq < OQV)
+                    outq[4 * dt + jq] = u32x2{E::pack(oacc[4 * jq + 0] * inv, oacc[4 * jq + 1] * inv),
+                                              E::pack(oacc[4 * jq + 2] * inv, oacc[4 * jq + 3] * inv)};
         }
-#pragma unroll
-        for (int i = 0; i < OQ; ++i) {
-            if (b) outq[1][i] = ocur[i];
-            else outq[0][i] = ocur[i];
-        }
+    };
+    u32x2 out0[OQV], out1[OQV];
+    if (active) {  // uniform within the wavefront; no barrier inside
+        tile(qop[0], out0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (L > 32) tile(qop[1], out1);
     }
-    __syncthreads();  // V^T is dead: the output rows go over it
+    __syncthreads();  // V is dead: the output rows go over it
 
-    // ---- 6. output rows through LDS, stored as coalesced slab rows --------------------
+    // ---- 5. output rows through LDS, stored as coalesced slab rows --------------------
     if (active) {
+        auto put = [&](const u32x2 (&outq)[OQV], int b) {
+            char *orow = oslab + (32 * b + r) * PITCH + w * (2 * D);
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            if (b * 32 < L) {
-                char *orow = oslab + (32 * b + r) * PITCH + w * (2 * D);
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-                    for (int jq = 0; jq < 4; ++jq) {
-                        const int d0 = 32 * dt + 8 * jq + 4 * g;
-                        if (d0 < D) *(u32x2 *)(orow + 2 * d0) = outq[b][4 * dt + jq];
-                    }
-                }
+            for (int i = 0; i < OQV; ++i) {
+                const int d0 = 32 * (i / 4) + 8 * (i % 4) + 4 * g;
+                if (d0 < D) *(u32x2 *)(orow + 2 * d0) = outq[i];
             }
-        }
+        };
+        put(out0, 0);
+        if (L > 32) put(out1, 1);
     }
     __syncthreads();
-    const int to = fresh(tid);
+    {
+        char *ob = p.out + ((int64_t)s0 * p.so_s + (int64_t)h0 * p.so_h) * 2;
+        const uint32_t ors = (uint32_t)p.so_s * 2, ohs = (uint32_t)p.so_h * 2;
+        auto store = [&](auto fast_tag) {
+            constexpr bool F = decltype(fast_tag)::value;
+            GridWalk<NCH> it(fresh(tid));
+            uint32_t oro = (uint32_t)it.row * ors;
 #pragma unroll
-    for (int k = 0; k < SPER; ++k) {
-        const int it = to + k * kWinThreads;
-        if (it < SITEMS) {
-            const int tok = it / NCH, wc = it - tok * NCH;
-            const int hh = wc / HCH, c = wc - hh * HCH;
-            if (tok < L && hh < nh)
-                *(u32x4 *)(ob + ((uint32_t)tok * ors + (uint32_t)hh * ohs + 16 * c)) =
-                    *(const u32x4 *)(oslab + tok * PITCH + 16 * wc);
-        }
+            for (int k = 0; k < SPER; ++k) {
+                const u32x4 val = *(const u32x4 *)(oslab + it.row * PITCH + 16 * it.col);
+                if constexpr (F) {
+                    __builtin_nontemporal_store(val, (u32x4 *)(ob + (oro + 16 * it.col)));
+                } else if (it.row < L && it.col < nh * HCH) {
+                    __builtin_nontemporal_store(val, (u32x4 *)(ob + ((uint32_t)it.row * ors + chunk_off(it.col, ohs))));
+                }
+                const bool cy = it.next();
+                if constexpr (F) oro += GridWalk<NCH>::Q * ors + (cy ? ors : 0u);
+            }
+        };
+        if (fast) store(BoolTag<true>{});
+        else store(BoolTag<false>{});
     }
 }
 
@@ -1453,6 +1534,7 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
     kp.tail_first = 0;
     kp.tail_split = 1;
     kp.ws = nullptr;
+    kp.dense_heads = a->q_stride_head == d && a->k_stride_head == d && a->v_stride_head == d && a->out_stride_head == d;
     if (window) {
         kp.qblocks = 1;
         grid = (int64_t)a->num_seqs * ((a->num_heads + kWinHeads - 1) / kWinHeads);
