@@ -685,13 +685,16 @@ __global__ __launch_bounds__(kWinThreads, (WinLds<D, FULL>::kWaves)) void window
 //
 // Staging.  Raw K rows, their cos/sin rows and V rows go from HBM straight to
 // LDS (global_load_lds_dwordx4: lane l of an instruction writes the 16 bytes
-// at LDS base + 16 l).  Each instruction moves one 16-byte column of a 64-row
-// block -- lane = row -- so LDS holds every staged block column-major in
-// 16-byte chunks ([chunk][row][16 B]) and a lane's global offset is just
-// row * row_stride.  K is rotated from LDS into a row-major K_rot buffer once
-// per block for all 256 query rows (wavefront w takes quads w, w + 8, ... of
-// all 64 rows).  V stays as loaded; ds_read_b64_tr_b16 reads it back
-// transposed into the A operand of O^T = V^T P^T.
+// at LDS base + 16 l).  Each staged block is row-major in LDS, a row of
+// 16-byte chunks padded to a pitch that keeps the reads below free of bank
+// conflicts, and an instruction moves 64 consecutive chunk slots: whole rows,
+// so that its global reads are coalesced (slots of the padding are not
+// loaded).  A lane's slot, and so its offset row * row_stride + 16 * chunk,
+// is the same in every block.  K is rotated from LDS into a row-major K_rot
+// buffer once per block for all query rows of the workgroup (wavefront w
+// takes quads w, w + kLongWaves, ... of all 64 rows).  V stays as loaded;
+// ds_read_b64_tr_b16 reads it back transposed into the A operand of
+// O^T = V^T P^T.
 //
 // Pipeline.  Iteration j overlaps matrix-core and vector work of one wavefront:
 //
@@ -727,6 +730,13 @@ constexpr int kLongThreads = 64 * kLongWaves;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
 constexpr int kLdsLimit = 160 * 1024;
 
+// Chunks of an LDS row of V: at least `need`, 4 or 12 mod 16.
+constexpr int long_vpitch(int need) {
+    int c = need;
+    while (c % 16 != 4 && c % 16 != 12) ++c;
+    return c;
+}
+
 template <int D, int RD, bool FULL> struct LongLds {
     static constexpr int RB = RD == FRA_DTYPE_F32 ? 4 : 2;
     static constexpr int HALF = D / 2;
@@ -736,15 +746,21 @@ template <int D, int RD, bool FULL> struct LongLds {
     static constexpr int NDT = (D + 31) / 32;          // 32-row tiles of O^T
     static constexpr int KCH = D / 8;                  // 16-byte chunks of a K or V row
     static constexpr int TCH = W * RB / 16;            // 16-byte chunks of a table row
-    static constexpr int VCOLS = 4 * NDT;              // V chunk columns read by the MFMAs
-    static constexpr int CST = 64 * 16;                // chunk column stride, raw K and tables
-    static constexpr int VCST = 64 * 16 + 64;          // chunk column stride of V (bank offset 16)
+    // Row pitches in 16-byte chunks.  Raw K and table rows: an odd number of
+    // chunks, so 16 consecutive rows start in 16 different 4-bank groups
+    // (16-byte reads conflict-free, 8-byte reads at most 2-way).  V rows:
+    // 4 or 12 mod 16 chunks (16 or 48 dwords mod 64), so the four rows a
+    // 16-lane group of a transposed read touches fall in disjoint banks; a
+    // row also holds the columns [D, 32 NDT) the last O^T tile reads.
+    static constexpr int KPC = KCH % 2 ? KCH : KCH + 1;
+    static constexpr int TPC = TCH % 2 ? TCH : TCH + 1;
+    static constexpr int VPC = long_vpitch(4 * NDT);
     static constexpr bool kOnesCol = D % 32 != 0;      // V column D holds ones
-    static constexpr int kRawK = KCH * CST;
-    static constexpr int kRawT = TCH * CST;
+    static constexpr int kRawK = 64 * KPC * 16;
+    static constexpr int kRawT = 64 * TPC * 16;
     static constexpr int kRaw = kRawK + 2 * kRawT;     // raw K, cos, sin of one block
     static constexpr int kKrot = kLongBKV * KS * 2;
-    static constexpr int kV = VCOLS * VCST;
+    static constexpr int kV = 64 * VPC * 16;
     static constexpr int kRawBufs = 2 * (kRaw + kKrot + kV) <= kLdsLimit ? 2 : 1;
     static constexpr int kOffKrot = kRawBufs * kRaw;
     static constexpr int kOffV = kOffKrot + 2 * kKrot;
@@ -755,13 +771,16 @@ template <int D, int RD, bool FULL> struct LongLds {
 
 // ---- split last round: partial results and their merge ------------------------
 //
-// Workspace: per (split unit, part), 256 rows of split_row_floats(D) floats:
+// Workspace: per (split unit, part), kLongBQ rows of split_row_floats(D) floats:
 // O (unnormalised, head_dim values), m (running max in scale*log2e units) and
 // l (row sum of P).  split_merge_kernel, launched after the long kernel on
 // the same stream, merges the parts of each unit into the output.
 constexpr int kSplitMaxParts = 8;
 
 __host__ __device__ constexpr int split_row_floats(int d) { return (d + 2 + 3) / 4 * 4; }  // 16-byte pitch
+
+// Workgroups (of 256 threads, one per (row, 4 columns)) of the merge per unit.
+__host__ __device__ constexpr int split_merge_blocks(int d) { return (kLongBQ * (d / 4) + 255) / 256; }
 
 inline int64_t split_workspace_bytes(int64_t units, int parts, int d) {
     return units * parts * kLongBQ * (int64_t)split_row_floats(d) * 4;
@@ -801,7 +820,8 @@ template <int D, class E>
 __global__ __launch_bounds__(256) void split_merge_kernel(const KParams p) {
     constexpr int RF = split_row_floats(D);
     constexpr int NC = D / 4;
-    const int tu = blockIdx.x / NC, blk = blockIdx.x - tu * NC;
+    constexpr int BPU = split_merge_blocks(D);  // workgroups per unit
+    const int tu = blockIdx.x / BPU, blk = blockIdx.x - tu * BPU;
     const int u = p.tail_first + tu, nparts = p.tail_split;
     const int sh = u / p.qblocks, qblk = u - sh * p.qblocks;
     const int seg = sh / p.num_heads, head = sh - seg * p.num_heads;
@@ -809,7 +829,8 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const KParams p) {
     s0 = min(max(s0, 0), p.total);
     s1 = min(max(s1, 0), p.total);
     const int L = s1 - s0;
-    const int it = blk * 256 + threadIdx.x;  // < kLongBQ * NC
+    const int it = blk * 256 + threadIdx.x;
+    if (it >= kLongBQ * NC) return;
     const int row = it / NC, c = it - row * NC;
     const int q = qblk * kLongBQ + row;
     if (L <= 0 || q >= L) return;
@@ -855,9 +876,9 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     constexpr int NDT = LDS::NDT;
     constexpr int RB = LDS::RB;
     constexpr int KCH = LDS::KCH, TCH = LDS::TCH;
-    constexpr int CST = LDS::CST, VCST = LDS::VCST;
-    constexpr int NRAWI = KCH + 2 * TCH;       // direct loads of one raw block
-    constexpr int NDMA = NRAWI + KCH;          // ... plus the V block
+    constexpr int KPC = LDS::KPC, TPC = LDS::TPC, VPC = LDS::VPC;
+    constexpr int NRAWI = KPC + 2 * TPC;       // direct loads of one raw block
+    constexpr int NDMA = NRAWI + VPC;          // ... plus the V block
     constexpr int MPER = (NDMA + kLongWaves - 1) / kLongWaves;
     constexpr int RPER = (NQ + kLongWaves - 1) / kLongWaves;  // rotation quads per wavefront
     constexpr bool ONES = LDS::kOnesCol;
@@ -915,49 +936,62 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     // V padding columns [D, 32*NDT) of both buffers: zero, column D ones.
     // They are never overwritten by the staging loads.
     {
-        constexpr int PADC = LDS::VCOLS - KCH;  // padding chunk columns
+        constexpr int PADC = VPC - KCH;  // padding chunks of a V row
         const u32 one = E::pack(1.0f, 0.0f) & 0xffffu;
-        for (int i = tid; i < 2 * PADC * 64; i += kLongThreads) {
-            const int bf = i / (PADC * 64), rem = i - bf * PADC * 64;
-            const int pc = rem / 64, row = rem - pc * 64;
+        for (int i = tid; i < 2 * 64 * PADC; i += kLongThreads) {
+            const int bf = i / (64 * PADC), rem = i - bf * 64 * PADC;
+            const int row = rem / PADC, pc = rem - row * PADC;
             u32x4 val = {0u, 0u, 0u, 0u};
             if (ONES && pc == 0) val[0] = one;  // element 0 of chunk D/8 is column D
-            *(u32x4 *)(lds + LDS::kOffV + bf * LDS::kV + (KCH + pc) * VCST + row * 16) = val;
+            *(u32x4 *)(lds + LDS::kOffV + bf * LDS::kV + row * (VPC * 16) + (KCH + pc) * 16) = val;
         }
     }
 
     // ---- direct-load jobs ---------------------------------------------------------
-    // A block is staged by NDMA direct loads, each moving one 16-byte chunk
-    // column of its 64 rows: raw K columns, cos columns, sin columns (the raw
-    // part), then V columns.  Wavefront w owns loads w, w + 8, ... (job m is
-    // load w + 8m).  Iteration j loads the raw part of block j + DIST and the
-    // V part of block j + 1.
+    // A block is staged by NDMA direct loads, each moving 64 consecutive
+    // 16-byte slots of one region: raw K (KPC loads), cos (TPC), sin (TPC)
+    // -- the raw part -- then V (VPC).  Slot s of a region with pitch PC is
+    // chunk s % PC of row s / PC; chunks past the row's data are padding and
+    // not loaded.  Wavefront w owns loads w, w + kLongWaves, ... (job m is
+    // load w + kLongWaves m).  Iteration j loads the raw part of block
+    // j + DIST and the V part of block j + 1.
     constexpr int MFULL = NDMA / kLongWaves;  // jobs every wavefront has
+    constexpr uint32_t kPadSlot = 0xffffffffu;
     struct Job {
-        const char *base;  // the job's chunk column in block 0
+        const char *base;  // the job's tensor at the first row of block 0
         uint32_t rows;     // row stride (bytes)
         uint32_t lds0;     // LDS destination in buffer 0
         uint32_t bufstep;  // bytes between LDS buffers
+        int row;           // this lane's row
+        uint32_t col;      // this lane's byte offset in the row, kPadSlot for padding
         bool raw;          // raw part (K, cos, sin) or V
     };
     auto job_desc = [&](int m) {
         const int gi = min(w + kLongWaves * m, NDMA - 1);
         Job jb;
-        if (gi < KCH) {
-            jb.base = kbase + 16 * gi;
+        auto slot = [&](int ii, int pc, int dc) {  // pc, dc: compile-time in each branch
+            const int s = 64 * ii + lane, row = s / pc, c = s - row * pc;
+            jb.row = row;
+            jb.col = c < dc ? (uint32_t)(16 * c) : kPadSlot;
+        };
+        if (gi < KPC) {
+            jb.base = kbase;
             jb.rows = (uint32_t)krs;
-            jb.lds0 = (uint32_t)(gi * CST);
+            jb.lds0 = (uint32_t)(gi * 1024);
+            slot(gi, KPC, KCH);
         } else if (gi < NRAWI) {
-            const bool is_cos = gi < KCH + TCH;
-            const int c = is_cos ? gi - KCH : gi - KCH - TCH;
-            jb.base = (is_cos ? cbase : sbase) + 16 * c;
+            const bool is_cos = gi < KPC + TPC;
+            const int ii = is_cos ? gi - KPC : gi - KPC - TPC;
+            jb.base = is_cos ? cbase : sbase;
             jb.rows = (uint32_t)trs;
-            jb.lds0 = (uint32_t)(LDS::kRawK + (is_cos ? 0 : LDS::kRawT) + c * CST);
+            jb.lds0 = (uint32_t)(LDS::kRawK + (is_cos ? 0 : LDS::kRawT) + ii * 1024);
+            slot(ii, TPC, TCH);
         } else {
-            const int c = gi - NRAWI;
-            jb.base = vbase + 16 * c;
+            const int ii = gi - NRAWI;
+            jb.base = vbase;
             jb.rows = (uint32_t)vrs;
-            jb.lds0 = (uint32_t)(LDS::kOffV + c * VCST);
+            jb.lds0 = (uint32_t)(LDS::kOffV + ii * 1024);
+            slot(ii, VPC, KCH);
         }
         jb.raw = gi < NRAWI;
         jb.bufstep = jb.raw ? LDS::kRaw : LDS::kV;
@@ -974,10 +1008,12 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         const int x = jb.raw ? xr : xv, bf = jb.raw ? br : bv;
         if (x >= nblk) return;
         const int nkv = min(kLongBKV, Lkv - kLongBKV * x);
-        const uint32_t voff = (uint32_t)min(lane, nkv - 1) * jb.rows;
-        const char *src = jb.base + (int64_t)x * kLongBKV * jb.rows;
-        __builtin_amdgcn_global_load_lds((glb_void *)(src + voff), (lds_void *)(lds + jb.lds0 + bf * jb.bufstep),
-                                         16, 0, 0);
+        if (jb.col != kPadSlot) {
+            const uint32_t voff = (uint32_t)min(jb.row, nkv - 1) * jb.rows + jb.col;
+            const char *src = jb.base + (int64_t)x * kLongBKV * jb.rows;
+            __builtin_amdgcn_global_load_lds((glb_void *)(src + voff), (lds_void *)(lds + jb.lds0 + bf * jb.bufstep),
+                                             16, 0, 0);
+        }
     };
     // The loads of iteration j (generic path).
     auto dma_iter = [&](int j) {
@@ -989,36 +1025,34 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     const char *jptr[MPER];
     uint32_t jstep[MPER], jdst[MPER][2], jvoff[MPER];
     auto job_steady = [&](int m, int P) {
-        __builtin_amdgcn_global_load_lds((glb_void *)(jptr[m] + jvoff[m]), (lds_void *)(lds + jdst[m][P]), 16, 0, 0);
+        if (jvoff[m] != kPadSlot)
+            __builtin_amdgcn_global_load_lds((glb_void *)(jptr[m] + jvoff[m]), (lds_void *)(lds + jdst[m][P]), 16, 0, 0);
         jptr[m] += jstep[m];
     };
 
     // ---- rotation of one raw block into K_rot ---------------------------------------
-    // Wavefront w rotates quads i = w, w + 8, ... of row `lane`: fp32 math with
-    // separately rounded products (reference fused_attn.py:385-390), rounded to
-    // the storage dtype.  Quad w exists for every wavefront (NQ >= 8); the
-    // later ones only for some.
+    // Wavefront w rotates quads i = w, w + kLongWaves, ... of row `lane`
+    // (rotate_quad: reference fused_attn.py:389-390), rounded to the storage
+    // dtype.
     auto rotate_one = [&](int rawbuf, int kbuf, int i) {
-        const char *raw = lds + rawbuf * LDS::kRaw;
-        const char *ct = raw + LDS::kRawK, *st = raw + LDS::kRawK + LDS::kRawT;
+        const char *raw = lds + rawbuf * LDS::kRaw + lane * (KPC * 16);
+        const char *ct = lds + rawbuf * LDS::kRaw + LDS::kRawK + lane * (TPC * 16);
+        const char *st = ct + LDS::kRawT;
         char *kr = lds + LDS::kOffKrot + kbuf * LDS::kKrot + lane * (KS * 2);
-        // byte offset within a row -> (chunk column, byte within chunk)
-        auto at = [&](const char *base, int byte) { return base + (byte >> 4) * CST + lane * 16 + (byte & 15); };
-        const u32x2 x0 = *(const u32x2 *)at(raw, 8 * i);
-        const u32x2 x1 = *(const u32x2 *)at(raw, D + 8 * i);
-        const f32x4 c0 = Rope<RD>::quad(at(ct, RB * 4 * i));
-        const f32x4 s0v = Rope<RD>::quad(at(st, RB * 4 * i));
+        const u32x2 x0 = *(const u32x2 *)(raw + 8 * i);
+        const u32x2 x1 = *(const u32x2 *)(raw + D + 8 * i);
+        const f32x4 c0 = Rope<RD>::quad(ct + RB * 4 * i);
+        const f32x4 s0v = Rope<RD>::quad(st + RB * 4 * i);
         f32x4 c1 = c0, s1v = s0v;
         if constexpr (FULL) {
-            c1 = Rope<RD>::quad(at(ct, RB * (HALF + 4 * i)));
-            s1v = Rope<RD>::quad(at(st, RB * (HALF + 4 * i)));
+            c1 = Rope<RD>::quad(ct + RB * (HALF + 4 * i));
+            s1v = Rope<RD>::quad(st + RB * (HALF + 4 * i));
         }
         u32x2 r0w, r1w;
         rotate_quad<E>(x0, x1, c0, s0v, c1, s1v, r0w, r1w);
         *(u32x2 *)(kr + 8 * i) = r0w;
         *(u32x2 *)(kr + D + 8 * i) = r1w;
     };
-    static_assert(NQ >= kLongWaves, "every wavefront rotates at least one quad");
     auto rotate_rest = [&](int rawbuf, int kbuf) {
 #pragma unroll
         for (int m = 1; m < RPER; ++m) {
@@ -1027,7 +1061,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         }
     };
     auto rotate = [&](int rawbuf, int kbuf) {
-        rotate_one(rawbuf, kbuf, w);
+        if (kLongWaves <= NQ || w < NQ) rotate_one(rawbuf, kbuf, w);
         rotate_rest(rawbuf, kbuf);
     };
 
@@ -1094,11 +1128,10 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     // Per-lane LDS byte offsets.  K_rot A operand of S^T: row 32a + r, elements
     // 16t + 8g.  V transposed reads: the 16-lane group G = lane >> 4 covers
     // keys 4g + e (e = (lane >> 2) & 3) and columns 16 (G & 1) + 4 (lane & 3) of
-    // each 32-column tile; column c lives in chunk c / 8 at byte 2 (c % 8).
+    // each 32-column tile.
     const uint32_t k_lane = (uint32_t)(LDS::kOffKrot + (r * KS + 8 * g) * 2);
-    const int vcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    const uint32_t v_lane =
-        (uint32_t)(LDS::kOffV + (vcol >> 3) * VCST + (4 * g + ((lane >> 2) & 3)) * 16 + (vcol & 7) * 2);
+    const uint32_t v_lane = (uint32_t)(LDS::kOffV + (4 * g + ((lane >> 2) & 3)) * (VPC * 16) +
+                                       2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
 
 
     // S^T of block x (K_rot buffer x & 1).
@@ -1181,12 +1214,12 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         const char *vb = lds + v_lane + (x & 1) * LDS::kV;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
-            const char *vrp = vb + 16 * st * 16;  // keys 16 st: 16 rows of 16 bytes
+            const char *vrp = vb + 16 * st * (VPC * 16);  // keys 16 st
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
-                const char *cp = vrp + 4 * dt * VCST;  // 32 columns = 4 chunk columns
+                const char *cp = vrp + 64 * dt;  // 32 columns
                 const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)cp);
-                const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(cp + 8 * 16));
+                const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(cp + 8 * (VPC * 16)));
                 const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
                 oacc[dt] = E::mma(u32x4{l2[0], l2[1], h2[0], h2[1]}, pop[st], oacc[dt]);
             }
@@ -1205,7 +1238,6 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     // the MFMAs with the softmax and rotation work; the generic variant checks.
     auto iteration_steady = [&](auto par_tag, int j, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
         constexpr int P = decltype(par_tag)::value;
-        u32x4 pop[4];
         smax(cur, kLongBKV);
         constexpr int RB2 = RAWBUFS == 2 ? P : 0;  // raw buffer of block j + 2
 #pragma unroll
@@ -1214,14 +1246,50 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
             // one raw buffer: every load of the iteration precedes the mid barrier
             if (has_job(MFULL)) job_steady(MFULL, P);
         }
-        qk(j + 1, nxt);
-        sexp(cur, pop);
+        __builtin_amdgcn_sched_barrier(0);
+        // Phase A, one MFMA of S(j+1) then about three exponentials of S(j)
+        // per step, so that the matrix core and the vector unit of this
+        // wave both stay busy (the two accumulator chains alternate, and the
+        // K_rot operand of a step is read two steps ahead).
+        {
+            constexpr int NA = 2 * S;
+            const char *kb = lds + k_lane + ((j + 1) & 1) * LDS::kKrot;
+            auto kaddr = [&](int i) { return kb + (i & 1) * (32 * KS * 2) + 32 * (i >> 1); };
+            u32x4 kr[3];
+            kr[0] = *(const u32x4 *)kaddr(0);
+            kr[1] = *(const u32x4 *)kaddr(1);
+            float lsum = 0.f;
+#pragma unroll
+            for (int i = 0; i < NA; ++i) {
+                if (i + 2 < NA) kr[(i + 2) % 3] = *(const u32x4 *)kaddr(i + 2);
+                const int ac = i & 1, tt = i >> 1;
+                nxt[ac] = E::mma(kr[i % 3], qop[tt], tt == 0 ? f32x16{} : nxt[ac]);
+#pragma unroll
+                for (int e = 32 * i / NA; e < 32 * (i + 1) / NA; ++e) {
+                    const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(cur[e >> 4][e & 15], sl, -m_i));
+                    cur[e >> 4][e & 15] = x;
+                    if constexpr (!ONES) lsum += x;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (!ONES) l_i += lsum + xchg32(lsum);
+        }
+        u32x4 pop[4];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                pop[2 * a + h] = u32x4{E::pack(cur[a][8 * h + 0], cur[a][8 * h + 1]),
+                                       E::pack(cur[a][8 * h + 2], cur[a][8 * h + 3]),
+                                       E::pack(cur[a][8 * h + 4], cur[a][8 * h + 5]),
+                                       E::pack(cur[a][8 * h + 6], cur[a][8 * h + 7])};
+        }
         if constexpr (RAWBUFS == 1) {
             wait_dma();
             __syncthreads();
         }
         pv(j, pop);
-        rotate_one(RB2, P, w);
+        if (kLongWaves <= NQ || w < NQ) rotate_one(RB2, P, w);
         if constexpr (RAWBUFS == 2 && MPER > MFULL) {
             if (has_job(MFULL)) job_steady(MFULL, P);
         }
@@ -1256,7 +1324,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
             const Job jb = job_desc(m);
             jstep[m] = kLongBKV * jb.rows;
             jptr[m] = jb.base + (int64_t)(jb.raw ? DIST : 1) * jstep[m];
-            jvoff[m] = (uint32_t)lane * jb.rows;
+            jvoff[m] = jb.col == kPadSlot ? kPadSlot : (uint32_t)jb.row * jb.rows + jb.col;
 #pragma unroll
             for (int P = 0; P < 2; ++P)
                 jdst[m][P] = jb.lds0 + (jb.raw ? (uint32_t)((P + DIST) % RAWBUFS) : (uint32_t)((P + 1) & 1)) * jb.bufstep;
@@ -1588,7 +1656,7 @@ int fra_fwd_varlen(const fra_fwd_args *args, void *stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(FRA_EHIP, "launch of %s failed: %s", c.name, hipGetErrorString(e));
     if (c.split_parts > 1) {
-        hipLaunchKernelGGL(c.merge, dim3(c.split_units * (args->head_dim / 4)), dim3(256), 0, (hipStream_t)stream, kp);
+        hipLaunchKernelGGL(c.merge, dim3(c.split_units * split_merge_blocks(args->head_dim)), dim3(256), 0, (hipStream_t)stream, kp);
         e = hipGetLastError();
         if (e != hipSuccess) return fail(FRA_EHIP, "launch of the merge of %s failed: %s", c.name, hipGetErrorString(e));
     }

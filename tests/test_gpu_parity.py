@@ -322,7 +322,7 @@ def _call_abi(case, device, workspace: bool):
 
 @pytest.mark.parametrize("lens,h,d", [([2000], 3, 80), ([700, 1500, 64, 1], 2, 72), ([9216], 16, 80)])
 def test_long_kernel_split_last_round(device, lens, h, d):
-    # the split path (parts of the key range merged in-kernel) against the
+    # the split path (parts of the key range merged by split_merge_kernel) against the
     # unsplit kernel and the oracle
     case = random_case(lens, h=h, d=d, seed=260 + d)
     split, pl = _call_abi(case, device, workspace=True)
