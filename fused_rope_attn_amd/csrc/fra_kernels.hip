@@ -212,8 +212,9 @@ __device__ __forceinline__ void load_rotate_quad(const char *xrow, const char *c
 
 // ---- window kernel ------------------------------------------------------------
 //
-// One workgroup of 4 wavefronts per (segment, group of 4 heads); segment
-// length L <= 64.  All HBM traffic is coalesced: consecutive lanes move
+// One workgroup of HW wavefronts per (segment, group of HW heads), HW = 4,
+// or 2 when a layer has too few windows to fill the chip; segment length
+// L <= 64.  All HBM traffic is coalesced: consecutive lanes move
 // consecutive 16-byte chunks of the group's slab -- 4 heads x D elements,
 // contiguous in a [tokens, heads, head_dim] tensor -- and LDS turns the slab
 // into MFMA operands (and the output back into slab rows).
@@ -245,8 +246,7 @@ __device__ __forceinline__ void load_rotate_quad(const char *xrow, const char *c
 // {x0r[4i..4i+3], x1r[4i..4i+3]} of quad i = g*S + t (the contraction order is
 // free as long as Q and K share it).
 
-constexpr int kWinHeads = 4;     // heads (wavefronts) per workgroup
-constexpr int kWinThreads = 64 * kWinHeads;
+constexpr int kWinHeadsMax = 4;  // heads (wavefronts) per workgroup, at most
 
 // Bytes of an LDS row of V: at least `need`, a multiple of 64 bytes, and
 // 16 or 48 dwords past a multiple of 64 dwords, so that the four rows one
@@ -257,10 +257,10 @@ constexpr int win_vpitch(int need) {
     return 4 * dw;
 }
 
-// The items first, first + kWinThreads, ... of a row-major [rows][N] grid as
-// (row, col), stepped without divisions: kWinThreads = Q*N + R.
-template <int N> struct GridWalk {
-    static constexpr int Q = kWinThreads / N, R = kWinThreads % N;
+// The items first, first + STEP, ... of a row-major [rows][N] grid as
+// (row, col), stepped without divisions: STEP = Q*N + R.
+template <int N, int STEP> struct GridWalk {
+    static constexpr int Q = STEP / N, R = STEP % N;
     int row, col;
     __device__ __forceinline__ explicit GridWalk(int first) : row(first / N), col(first - (first / N) * N) {}
     // Advances to the next item; true when the column wrapped (one more row).
@@ -279,15 +279,15 @@ template <bool B> struct BoolTag {
     static constexpr bool value = B;
 };
 
-template <int D, bool FULL> struct WinLds {
+template <int D, bool FULL, int HW> struct WinLds {
     static constexpr int W = FULL ? D : D / 2;         // table width
     static constexpr int CS = 2 * W + 4;               // fp32 per [cos | sin] row, +4 pad (conflict-free b128 reads)
-    static constexpr int SLAB = kWinHeads * D * 2;     // bytes of one token's slab
+    static constexpr int SLAB = HW * D * 2;            // bytes of one token's slab
     static constexpr int PITCH = SLAB + 16;            // LDS row pitch of a staged slab (one pad chunk)
     static constexpr int NDT = (D + 31) / 32;          // 32-row tiles of O^T
     // A V row holds the slab and the columns the last head's padding tile
     // reads past it (values only reach discarded output rows).
-    static constexpr int VNEED = 2 * ((kWinHeads - 1) * D + 32 * NDT) > SLAB ? 2 * ((kWinHeads - 1) * D + 32 * NDT) : SLAB;
+    static constexpr int VNEED = 2 * ((HW - 1) * D + 32 * NDT) > SLAB ? 2 * ((HW - 1) * D + 32 * NDT) : SLAB;
     static constexpr int VP = win_vpitch(VNEED);
     static constexpr int VPC = VP / 16;                // 16-byte slots per V row
     static constexpr int kTableBytes = 32 * CS * 4;    // tables of one 32-token half
@@ -303,11 +303,15 @@ template <int D, bool FULL> struct WinLds {
     // leave room (half-width tables, D = 64 or 80: at most 166 VGPRs without
     // spills), else two.
     static constexpr int kWaves = !FULL && D <= 80 && D % 16 == 0 && 3 * kBytes <= 160 * 1024 ? 3 : 2;
+    // Workgroups per CU (LDS and wavefronts per SIMD), for the planner.
+    static constexpr int kPerCu = (160 * 1024 / kBytes) < (4 * kWaves / HW) ? (160 * 1024 / kBytes) : (4 * kWaves / HW);
 };
 
-template <int D, class E, int RD, bool FULL>
-__global__ __launch_bounds__(kWinThreads, (WinLds<D, FULL>::kWaves)) void window_kernel(const KParams p) {
-    using LDS = WinLds<D, FULL>;
+template <int D, class E, int RD, bool FULL, int HW>
+__global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window_kernel(const KParams p) {
+    using LDS = WinLds<D, FULL, HW>;
+    constexpr int kWinHeads = HW;
+    constexpr int kWinThreads = 64 * HW;
     constexpr int NQ = D / 8;                 // quads per half
     constexpr int S = (NQ + 1) / 2;           // 16-deep k-steps of QK^T
     constexpr int NDT = LDS::NDT;
@@ -317,8 +321,6 @@ __global__ __launch_bounds__(kWinThreads, (WinLds<D, FULL>::kWaves)) void window
     constexpr int VP = LDS::VP, VPC = LDS::VPC;
     constexpr int HCH = D / 8;                // 16-byte chunks per head row
     constexpr int NCH = kWinHeads * HCH;      // chunks per slab row
-    constexpr int SLABB = LDS::SLAB;          // bytes of one token's slab
-    static_assert(SLABB % 64 == 0, "slab rows are whole 64-byte sectors");
     constexpr int RB = Rope<RD>::kBytes;
     constexpr int TQ = W / 4;                 // table quads per row
     constexpr int TN = 2 * TQ;                // table items per token: cos quads, then sin quads
@@ -383,7 +385,7 @@ __global__ __launch_bounds__(kWinThreads, (WinLds<D, FULL>::kWaves)) void window
     // 144-window layer).
     f32x4 tv[TPER];
     {
-        GridWalk<TN> it(fresh(tid));
+        GridWalk<TN, kWinThreads> it(fresh(tid));
 #pragma unroll
         for (int k = 0; k < TPER; ++k) {
             const int tok = min(it.row, 63), c = it.col;
@@ -399,7 +401,7 @@ __global__ __launch_bounds__(kWinThreads, (WinLds<D, FULL>::kWaves)) void window
         const uint32_t qhs = (uint32_t)p.sq_h * 2, khs = (uint32_t)p.sk_h * 2;
         auto load_slabs = [&](auto fast_tag) {
             constexpr bool F = decltype(fast_tag)::value;
-            GridWalk<NCH> it(fresh(tid));
+            GridWalk<NCH, kWinThreads> it(fresh(tid));
             uint32_t qro = (uint32_t)it.row * qrs, kro = (uint32_t)it.row * krs;
 #pragma unroll
             for (int k = 0; k < SPER; ++k) {
@@ -413,8 +415,8 @@ __global__ __launch_bounds__(kWinThreads, (WinLds<D, FULL>::kWaves)) void window
                 }
                 const bool cy = it.next();
                 if constexpr (F) {
-                    qro += GridWalk<NCH>::Q * qrs + (cy ? qrs : 0u);
-                    kro += GridWalk<NCH>::Q * krs + (cy ? krs : 0u);
+                    qro += GridWalk<NCH, kWinThreads>::Q * qrs + (cy ? qrs : 0u);
+                    kro += GridWalk<NCH, kWinThreads>::Q * krs + (cy ? krs : 0u);
                 }
             }
         };
@@ -428,7 +430,7 @@ __global__ __launch_bounds__(kWinThreads, (WinLds<D, FULL>::kWaves)) void window
     // wait for every outstanding load): items of the other half go to the
     // trash slot unless the half is known per item at compile time.
     auto stage_tab = [&](int hf) {
-        GridWalk<TN> it(fresh(tid));
+        GridWalk<TN, kWinThreads> it(fresh(tid));
 #pragma unroll
         for (int k = 0; k < TPER; ++k) {
             const bool in = (TITEMS % kWinThreads == 0 || it.row < 64) && (it.row >> 5) == hf;
@@ -439,7 +441,7 @@ __global__ __launch_bounds__(kWinThreads, (WinLds<D, FULL>::kWaves)) void window
         }
     };
     auto stage_half = [&](const u32x4 (&x)[SPER], int hf) {
-        GridWalk<NCH> it(fresh(tid));
+        GridWalk<NCH, kWinThreads> it(fresh(tid));
 #pragma unroll
         for (int k = 0; k < SPER; ++k) {
             char *dst = half + (it.row - 32 * hf) * PITCH + 16 * it.col;
@@ -505,7 +507,7 @@ __global__ __launch_bounds__(kWinThreads, (WinLds<D, FULL>::kWaves)) void window
         const uint32_t vrs = (uint32_t)p.sv_s * 2, vhs = (uint32_t)p.sv_h * 2;
         auto load_v = [&](auto fast_tag) {
             constexpr bool F = decltype(fast_tag)::value;
-            GridWalk<VPC> it(fresh(tid));  // slot 64 (w + 4k) + lane
+            GridWalk<VPC, kWinThreads> it(fresh(tid));  // slot 64 (w + HW k) + lane
             uint32_t vro = (uint32_t)it.row * vrs;
 #pragma unroll
             for (int k = 0; k < VPER; ++k) {
@@ -519,7 +521,7 @@ __global__ __launch_bounds__(kWinThreads, (WinLds<D, FULL>::kWaves)) void window
                     }
                 }
                 const bool cy = it.next();
-                if constexpr (F) vro += GridWalk<VPC>::Q * vrs + (cy ? vrs : 0u);
+                if constexpr (F) vro += GridWalk<VPC, kWinThreads>::Q * vrs + (cy ? vrs : 0u);
             }
         };
         if (fast) load_v(BoolTag<true>{});
@@ -658,7 +660,7 @@ __global__ __launch_bounds__(kWinThreads, (WinLds<D, FULL>::kWaves)) void window
         const uint32_t ors = (uint32_t)p.so_s * 2, ohs = (uint32_t)p.so_h * 2;
         auto store = [&](auto fast_tag) {
             constexpr bool F = decltype(fast_tag)::value;
-            GridWalk<NCH> it(fresh(tid));
+            GridWalk<NCH, kWinThreads> it(fresh(tid));
             uint32_t oro = (uint32_t)it.row * ors;
 #pragma unroll
             for (int k = 0; k < SPER; ++k) {
@@ -669,7 +671,7 @@ __global__ __launch_bounds__(kWinThreads, (WinLds<D, FULL>::kWaves)) void window
                     __builtin_nontemporal_store(val, (u32x4 *)(ob + ((uint32_t)it.row * ors + chunk_off(it.col, ohs))));
                 }
                 const bool cy = it.next();
-                if constexpr (F) oro += GridWalk<NCH>::Q * ors + (cy ? ors : 0u);
+                if constexpr (F) oro += GridWalk<NCH, kWinThreads>::Q * ors + (cy ? ors : 0u);
             }
         };
         if (fast) store(BoolTag<true>{});
@@ -1395,6 +1397,8 @@ struct Choice {
     KernelFn fn;
     KernelFn merge;  // split_merge_kernel of the long kernel's instance
     int kernel, grid, block, block_q, block_kv, lds, split_units, split_parts;
+    int heads;       // window kernel: heads (wavefronts) per workgroup
+    int per_cu;      // window kernel: workgroups resident per CU
     char name[64];
 };
 
@@ -1450,12 +1454,20 @@ template <int D, int RD, bool FULL> constexpr bool long_ok() {
     return (FULL ? D : D / 2) * (RD == FRA_DTYPE_F32 ? 4 : 2) % 16 == 0;
 }
 
-template <int D, class E, int RD, bool FULL> void pick_full(bool window, Choice &c) {
+template <int D, class E, int RD, bool FULL> void pick_full(bool window, int hw, Choice &c) {
     c.fn = nullptr;
     if constexpr (D <= kWindowMaxD) {
         if (window) {
-            c.fn = (KernelFn)window_kernel<D, E, RD, FULL>;
-            c.lds = WinLds<D, FULL>::kBytes;
+            if (hw == 2) {
+                c.fn = (KernelFn)window_kernel<D, E, RD, FULL, 2>;
+                c.lds = WinLds<D, FULL, 2>::kBytes;
+                c.per_cu = WinLds<D, FULL, 2>::kPerCu;
+            } else {
+                c.fn = (KernelFn)window_kernel<D, E, RD, FULL, 4>;
+                c.lds = WinLds<D, FULL, 4>::kBytes;
+                c.per_cu = WinLds<D, FULL, 4>::kPerCu;
+            }
+            c.heads = hw;
             return;
         }
     }
@@ -1466,33 +1478,33 @@ template <int D, class E, int RD, bool FULL> void pick_full(bool window, Choice 
     }
 }
 
-template <int D, class E, int RD> void pick_rd(bool window, bool full, Choice &c) {
-    if (full) pick_full<D, E, RD, true>(window, c);
-    else pick_full<D, E, RD, false>(window, c);
+template <int D, class E, int RD> void pick_rd(bool window, int hw, bool full, Choice &c) {
+    if (full) pick_full<D, E, RD, true>(window, hw, c);
+    else pick_full<D, E, RD, false>(window, hw, c);
 }
 
-template <int D> bool pick_d(bool window, bool full, int qkv, int rd, Choice &c) {
+template <int D> bool pick_d(bool window, int hw, bool full, int qkv, int rd, Choice &c) {
     if (qkv == FRA_DTYPE_BF16) {
-        if (rd == FRA_DTYPE_F32) pick_rd<D, BF16, FRA_DTYPE_F32>(window, full, c);
-        else if (rd == FRA_DTYPE_BF16) pick_rd<D, BF16, FRA_DTYPE_BF16>(window, full, c);
-        else pick_rd<D, BF16, FRA_DTYPE_F16>(window, full, c);
+        if (rd == FRA_DTYPE_F32) pick_rd<D, BF16, FRA_DTYPE_F32>(window, hw, full, c);
+        else if (rd == FRA_DTYPE_BF16) pick_rd<D, BF16, FRA_DTYPE_BF16>(window, hw, full, c);
+        else pick_rd<D, BF16, FRA_DTYPE_F16>(window, hw, full, c);
     } else {
-        if (rd == FRA_DTYPE_F32) pick_rd<D, F16, FRA_DTYPE_F32>(window, full, c);
-        else if (rd == FRA_DTYPE_BF16) pick_rd<D, F16, FRA_DTYPE_BF16>(window, full, c);
-        else pick_rd<D, F16, FRA_DTYPE_F16>(window, full, c);
+        if (rd == FRA_DTYPE_F32) pick_rd<D, F16, FRA_DTYPE_F32>(window, hw, full, c);
+        else if (rd == FRA_DTYPE_BF16) pick_rd<D, F16, FRA_DTYPE_BF16>(window, hw, full, c);
+        else pick_rd<D, F16, FRA_DTYPE_F16>(window, hw, full, c);
     }
     return true;
 }
 
 // Head dims with compiled kernels.  Each must be a multiple of 8 so that
 // both halves of a row start on an 8-byte boundary.
-bool pick_kernel(int d, bool window, bool full, int qkv, int rd, Choice &c) {
+bool pick_kernel(int d, bool window, int hw, bool full, int qkv, int rd, Choice &c) {
     switch (d) {
-        case 64: return pick_d<64>(window, full, qkv, rd, c);
-        case 72: return pick_d<72>(window, full, qkv, rd, c);
-        case 80: return pick_d<80>(window, full, qkv, rd, c);
-        case 96: return pick_d<96>(window, full, qkv, rd, c);
-        case 128: return pick_d<128>(window, full, qkv, rd, c);
+        case 64: return pick_d<64>(window, hw, full, qkv, rd, c);
+        case 72: return pick_d<72>(window, hw, full, qkv, rd, c);
+        case 80: return pick_d<80>(window, hw, full, qkv, rd, c);
+        case 96: return pick_d<96>(window, hw, full, qkv, rd, c);
+        case 128: return pick_d<128>(window, hw, full, qkv, rd, c);
         default: return false;
     }
 }
@@ -1540,7 +1552,7 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
     const bool small_rows = 64 * max_row_bytes < ((int64_t)1 << 31) && 64 * 4 * a->rope_stride_seq < ((int64_t)1 << 31);
     const bool window = a->max_seqlen <= 64 && d <= kWindowMaxD && small_rows;
     memset(&c, 0, sizeof(c));
-    if (!pick_kernel(d, window, a->rope_width == d, a->qkv_dtype, a->rope_dtype, c))
+    if (!pick_kernel(d, window, kWinHeadsMax, a->rope_width == d, a->qkv_dtype, a->rope_dtype, c))
         return fail(FRA_EUNSUPPORTED, "head_dim=%d has no compiled kernel (built: 64, 72, 80, 96, 128)", d);
     if (!c.fn)
         return fail(FRA_EUNSUPPORTED,
@@ -1604,10 +1616,20 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
     kp.ws = nullptr;
     kp.dense_heads = a->q_stride_head == d && a->k_stride_head == d && a->v_stride_head == d && a->out_stride_head == d;
     if (window) {
+        // Two heads per workgroup when that grid still runs in one round of
+        // resident workgroups (shorter per-workgroup chains: measured 2.6%
+        // faster at 144 windows x 16 heads, 4% at 16 windows), else four.
+        {
+            const int64_t g2 = (int64_t)a->num_seqs * ((a->num_heads + 1) / 2);
+            Choice c2;
+            memset(&c2, 0, sizeof(c2));
+            pick_kernel(d, true, 2, a->rope_width == d, a->qkv_dtype, a->rope_dtype, c2);
+            if (g2 <= (int64_t)device_cus() * c2.per_cu) c = c2;
+        }
         kp.qblocks = 1;
-        grid = (int64_t)a->num_seqs * ((a->num_heads + kWinHeads - 1) / kWinHeads);
+        grid = (int64_t)a->num_seqs * ((a->num_heads + c.heads - 1) / c.heads);
         c.kernel = FRA_KERNEL_WINDOW;
-        c.block = kWinThreads;
+        c.block = 64 * c.heads;
         c.block_q = 64;
         c.block_kv = 64;
         snprintf(c.name, sizeof(c.name), "window_d%d_%s_rope%s", d, dtype_name(a->qkv_dtype),
@@ -1703,7 +1725,7 @@ int fra_query_plan(const fra_fwd_args *args, fra_plan *out) {
 
 int fra_supports_head_dim(int32_t head_dim) {
     Choice c;
-    return pick_kernel(head_dim, true, false, FRA_DTYPE_BF16, FRA_DTYPE_F32, c) ? 1 : 0;
+    return pick_kernel(head_dim, true, kWinHeadsMax, false, FRA_DTYPE_BF16, FRA_DTYPE_F32, c) ? 1 : 0;
 }
 
 const char *fra_last_error(void) { return g_err; }

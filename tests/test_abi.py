@@ -66,10 +66,17 @@ def plan_of(a):
 def test_plan_window_and_long():
     rc, p = plan_of(make_args())
     assert rc == _lib.FRA_OK
-    # one workgroup of 4 wavefronts per (window, group of 4 heads)
-    assert p.kernel == _lib.FRA_KERNEL_WINDOW and p.grid == 16 * 4 and p.block == 256
+    # one workgroup of hw wavefronts per (window, group of hw heads): hw = 2
+    # when that grid runs in one round of resident workgroups (5 per CU, 256
+    # CUs assumed without a GPU), else 4
+    assert p.kernel == _lib.FRA_KERNEL_WINDOW and p.block == 128
+    assert p.grid == 16 * (16 // 2)
     rc, p = plan_of(make_args(h=6))  # a partial head group
-    assert rc == _lib.FRA_OK and p.grid == 16 * 2
+    assert rc == _lib.FRA_OK and p.grid == 16 * 3
+    rc, p = plan_of(make_args(n=9216, nseg=144))  # 1152 two-head workgroups fit 1280 slots
+    assert rc == _lib.FRA_OK and p.block == 128 and p.grid == 144 * 8
+    rc, p = plan_of(make_args(n=11968, nseg=187))  # 1496 do not: four heads
+    assert rc == _lib.FRA_OK and p.block == 256 and p.grid == 187 * 4
     assert p.name.decode() == "window_d80_bf16_ropef32"
     rc, p = plan_of(make_args(max_seqlen=9216, num_seqs=1, n=9216))
     assert rc == _lib.FRA_OK and p.kernel == _lib.FRA_KERNEL_LONG

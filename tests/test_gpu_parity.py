@@ -208,6 +208,28 @@ def test_out_argument_and_strided_views(device):
     assert torch.count_nonzero(wide[:, 1::2]) == 0
 
 
+@pytest.mark.parametrize("lens", [[64, 64, 64], [64, 40, 64]])
+def test_window_input_head_strides(device, lens):
+    # q/k/v whose head stride is not head_dim (every other head of a wider
+    # tensor) take the window kernel's general addressing path, also for full
+    # windows of four heads; the result must equal that of contiguous inputs
+    base = random_case(lens, h=4, d=80, seed=710 + len(lens) + lens[1])
+    ref = run_gpu(base, device)
+
+    def every_other_head(x):
+        wide = torch.zeros(x.shape[0], 2 * x.shape[1], x.shape[2], dtype=x.dtype, device=device)
+        wide[:, ::2] = x.to(device)
+        return wide[:, ::2]
+
+    q, k, v = (every_other_head(base[x]) for x in ("q", "k", "v"))
+    assert q.stride(1) == 2 * 80
+    cos, sin, cu = (base[x].to(device) for x in ("cos", "sin", "cu_seqlens"))
+    assert plan(q, k, v, cos, sin, cu, max_seqlen=64)["kernel"] == "window"
+    out = fused_rope_attention(q, k, v, cos, sin, cu, 64)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
 def test_rows_outside_segments_untouched_and_zero_path(device):
     case = random_case([10, 20], h=2, d=80, seed=800)
     q = case["q"].to(device)
