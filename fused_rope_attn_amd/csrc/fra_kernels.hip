@@ -135,10 +135,37 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
     return xcd < rem ? xcd * (base + 1) + local : rem * (base + 1) + (xcd - rem) * base + local;
 }
 
-// Value held by lane (lane ^ 32).
-__device__ __forceinline__ float xchg32(float x) {
-    const int lane = threadIdx.x & 63;
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, x)));
+// v_permlane32_swap with both operands in a and b: lanes 32..63 of a trade
+// places with lanes 0..31 of b, so when both start as x, one of them holds
+// x of lanes 0..31 in both halves and the other x of lanes 32..63.  It is a
+// VALU op: no LDS round trip (and no wait on other LDS reads in flight) on
+// the softmax's critical path.  The clang builtin of this toolchain returns
+// the first register for both results, hence the asm; the s_nop gives the
+// two wait states a VALU write needs before the permlane reads it.
+__device__ __forceinline__ void permlane32_swap(float &a, float &b) {
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+// max and sum of x over lanes l and l ^ 32 (symmetric, so the result does
+// not depend on which operand receives which half).
+__device__ __forceinline__ float max_pair32(float x) {
+    float a = x, b = x;
+    permlane32_swap(a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_pair32(float x) {
+    float a = x, b = x;
+    permlane32_swap(a, b);
+    return a + b;
+}
+
+// x of lane (l & 31) in every lane l: the upper half is zeroed first, so the
+// sum of the two swapped registers is the lower half's value whichever
+// register it lands in.
+__device__ __forceinline__ float bcast_lo32(float x) {
+    float a = (threadIdx.x & 32) ? 0.f : x, b = a;
+    permlane32_swap(a, b);
+    return a + b;
 }
 
 // max(a, b, c) in one instruction (the compiler only forms v_max3_f32 under
@@ -581,7 +608,7 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
         t8[10] = fmaxf(sacc[1][14], sacc[1][15]);
         float mx = fmaxf(max3f(max3f(t8[0], t8[1], t8[2]), max3f(t8[3], t8[4], t8[5]), max3f(t8[6], t8[7], t8[8])),
                          fmaxf(t8[9], t8[10]));
-        mx = fmaxf(mx, xchg32(mx));
+        mx = max_pair32(mx);
         const float mneg = -mx * sl;
         float lsum = 0.f;
 #pragma unroll
@@ -593,7 +620,7 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
                 lsum += e;
             }
         }
-        lsum += xchg32(lsum);
+        lsum = sum_pair32(lsum);
         const float inv = 1.0f / lsum;
 
         // P^T as the B operand of O^T = V^T P^T: step (a, h) uses elements
@@ -1174,7 +1201,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         const float u0 = max3f(t[0], t[1], t[2]), u1 = max3f(t[3], t[4], t[5]);
         const float u2 = max3f(t[6], t[7], t[8]), u3 = fmaxf(t[9], t[10]);
         float mx = fmaxf(max3f(u0, u1, u2), u3);
-        mx = fmaxf(mx, xchg32(mx)) * sl;
+        mx = max_pair32(mx) * sl;
         if (__builtin_amdgcn_ballot_w64(mx > m_i + kRescaleThreshold) != 0) {
             const float m_new = fmaxf(m_i, mx);
             const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
@@ -1198,7 +1225,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
                 if constexpr (!ONES) lsum += e;
             }
         }
-        if constexpr (!ONES) l_i += lsum + xchg32(lsum);
+        if constexpr (!ONES) l_i += sum_pair32(lsum);
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
 #pragma unroll
@@ -1274,7 +1301,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if constexpr (!ONES) l_i += lsum + xchg32(lsum);
+            if constexpr (!ONES) l_i += sum_pair32(lsum);
         }
         u32x4 pop[4];
 #pragma unroll
@@ -1348,8 +1375,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         // the last d tile, held by the g = 0 lanes.
         constexpr int jl = 4 * ((D - 32 * (NDT - 1)) / 8);
         const float lv = oacc[NDT - 1][jl];
-        const float lo = xchg32(lv);
-        l_i = g ? lo : lv;
+        l_i = bcast_lo32(lv);
     }
     const int q = qblk * kLongBQ + 32 * w + r;
     if (nparts > 1) {
