@@ -24,7 +24,7 @@ FRA_KERNEL_NONE = 0
 FRA_KERNEL_WINDOW = 1
 FRA_KERNEL_LONG = 2
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class FwdArgs(ctypes.Structure):
@@ -59,7 +59,22 @@ class FwdArgs(ctypes.Structure):
         ("flags", ctypes.c_int32),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_int64),
+        ("lse", ctypes.c_void_p),
     ]
+
+
+class BwdArgs(ctypes.Structure):
+    """Mirror of ``struct fra_bwd_args``."""
+
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("q", "k", "v", "cos", "sin", "out", "dout", "lse", "cu_seqlens", "dq", "dk", "dv")] + \
+               [(f"{t}_stride_{ax}", ctypes.c_int64) for t in ("q", "k", "v", "out", "dout", "dq", "dk", "dv")
+                for ax in ("seq", "head")] + \
+               [("rope_stride_seq", ctypes.c_int64)] + \
+               [(n, ctypes.c_int32) for n in ("total_seq", "num_heads", "head_dim", "num_seqs", "max_seqlen",
+                                              "rope_width", "qkv_dtype", "rope_dtype")] + \
+               [("softmax_scale", ctypes.c_float), ("flags", ctypes.c_int32),
+                ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64)]
 
 
 class Plan(ctypes.Structure):
@@ -89,6 +104,9 @@ SIGNATURES = {
     "fra_abi_version": (ctypes.c_int32, []),
     "fra_sizeof_args": (ctypes.c_int32, []),
     "fra_sizeof_plan": (ctypes.c_int32, []),
+    "fra_bwd_varlen": (ctypes.c_int, [ctypes.POINTER(BwdArgs), ctypes.c_void_p]),
+    "fra_bwd_workspace_bytes": (ctypes.c_int, [ctypes.POINTER(BwdArgs), ctypes.POINTER(ctypes.c_int64)]),
+    "fra_sizeof_bwd_args": (ctypes.c_int32, []),
 }
 
 _lib = None
@@ -125,7 +143,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
             fn.argtypes = args
         if lib.fra_abi_version() != ABI_VERSION:
             raise RuntimeError(f"libfra ABI {lib.fra_abi_version()} != expected {ABI_VERSION}")
-        if lib.fra_sizeof_args() != ctypes.sizeof(FwdArgs) or lib.fra_sizeof_plan() != ctypes.sizeof(Plan):
+        if (lib.fra_sizeof_args() != ctypes.sizeof(FwdArgs) or lib.fra_sizeof_plan() != ctypes.sizeof(Plan)
+                or lib.fra_sizeof_bwd_args() != ctypes.sizeof(BwdArgs)):
             raise RuntimeError("libfra struct layout does not match the ctypes mirror")
         _lib = lib
         return lib

@@ -1,0 +1,658 @@
+// fra_bwd.hip -- gfx950 backward of the fused RoPE + varlen attention op.
+//
+// The reference is forward-only (fused_attn.py:139-423 has no autograd and
+// no softmax statistics output).  This file adds the training side of the
+// same op, as the gradient of the forward's arithmetic (reference
+// fused_attn.py:316-423): with q_rot = rot(q), k_rot = rot(k) (fp32 rotation
+// rounded to the storage dtype), z = scale * q_rot k_rot^T per segment,
+// P = softmax(z), out = P v:
+//
+//   Dvec = rowsum(dout * out)                      (bwd_dot_kernel)
+//   dz   = P * (dout v^T - Dvec)
+//   dq   = rot^T(scale * dz k_rot)                 (bwd_dq_kernel)
+//   dk   = rot^T(scale * dz^T q_rot),  dv = P^T dout   (bwd_dkdv_kernel)
+//
+// where rot^T is the transpose of the per-pair rotation (the rounding of
+// q_rot / k_rot is taken as the identity, as autograd does for a cast).  P is
+// recomputed from the forward's log-sum-exp: P = exp2(z log2(e) - lse log2(e)).
+//
+// Both matrix kernels use v_mfma_f32_32x32x16_{bf16,f16} with the operand
+// layouts of the forward (fra_kernels.hip):
+//   bwd_dq_kernel    one workgroup per block of 32*NW queries; lane (r, g) of
+//                    wave w holds query 32w + r as the column of S^T, dP^T and
+//                    dQ^T (the forward's layout), looping over 64-key blocks of
+//                    K_rot and V staged in LDS.  dQ^T = K_rot^T dZ^T takes its
+//                    A operand from K_rot by ds_read_b64_tr_b16.
+//   bwd_dkdv_kernel  one workgroup per block of 32*NW keys; lane (r, g) holds
+//                    key 32w + r as the column of S = Q_rot K_rot^T and
+//                    dP = dout V^T, looping over 64-query blocks of Q_rot and
+//                    dout staged in LDS; dV^T = dout^T P and dK^T = Q_rot^T dZ
+//                    take their A operands from dout and Q_rot by transposed
+//                    reads.
+// dq and dk leave through LDS as fp32 rows, where the inverse rotation pairs
+// d with d + head_dim/2.  No atomics: every output row has one writer.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "fra.h"
+#include "fra_device.h"
+
+namespace {
+
+// Kernel parameters, passed by value.  Strides are in elements.
+struct BParams {
+    const char *q, *k, *v, *cos, *sin, *out, *dout;
+    const float *lse;
+    const int32_t *cu;
+    char *dq, *dk, *dv;
+    float *dvec;  // [num_heads, total]: rowsum(dout * out)
+    int64_t sq_s, sq_h, sk_s, sk_h, sv_s, sv_h, so_s, so_h, sdo_s, sdo_h;
+    int64_t sdq_s, sdq_h, sdk_s, sdk_h, sdv_s, sdv_h, sr_s;
+    int32_t total, num_heads, num_seqs;
+    int32_t blocks;    // row blocks per (segment, head) of the launched kernel
+    float scale;       // softmax_scale
+    float scale_log2;  // softmax_scale * log2(e)
+};
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+__host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
+__host__ __device__ constexpr int bwd_dp(int d) { return (d + 15) / 16 * 16; }
+
+// LDS row pitch (bytes) of a region read both as rows (16-byte reads) and
+// transposed (ds_read_b64_tr_b16): 4 or 12 mod 16 chunks of 16 bytes (16 or
+// 48 mod 64 dwords) keeps the transposed reads conflict-free.
+__host__ __device__ constexpr int bwd_pitch_tr(int d) {
+    int c = bwd_dp(d) / 8;
+    while (c % 16 != 4 && c % 16 != 12) ++c;
+    return 16 * c;
+}
+// ... and of a region read only as rows: an odd chunk count.
+__host__ __device__ constexpr int bwd_pitch_rows(int d) { return 16 * (bwd_dp(d) / 8 + 1); }
+// fp32 rows of the final transposes (dq, dk before the inverse rotation).
+__host__ __device__ constexpr int bwd_pitch_f32(int d) { return 4 * (d + 4); }
+
+// Wavefronts per SIMD the register budget of a backward kernel is sized for
+// (two: up to 256 VGPR + AGPR per lane; one at head_dim 128, whose dk/dv
+// accumulators alone take 128).
+template <int D> struct BwdOcc {
+    static constexpr int kWaves = D >= 128 ? 1 : 2;
+};
+
+constexpr int kBwdBlockQ = 64;   // queries per LDS stage of the dk/dv kernel
+constexpr int kBwdBlockKV = 64;  // keys per LDS stage of the dq kernel
+
+// Rows [0, nrows) of a block whose row 0 is token tok0 of x: the split-half
+// rotation (fp32, rounded to the storage dtype, as the forward computes it)
+// into LDS rows [x0r | x1r | 0-pad to a multiple of 16].  Rows >= nvalid are
+// zero.  x points at token tok0's row of the head; xs is its row stride in
+// bytes.
+template <int D, class E, bool FULL>
+__device__ __forceinline__ void stage_rotated(char *dst, int pitch, const BParams &p, const char *x, int64_t xs,
+                                              int tok0, int nvalid, int nrows, int tid, int nthr) {
+    constexpr int NQ = D / 8;  // quads per half
+    constexpr int HALF = D / 2;
+    constexpr int PADQ = (bwd_dp(D) - D) / 4;
+    constexpr int PER = NQ + PADQ;
+    for (int it = tid; it < nrows * PER; it += nthr) {
+        const int row = it / PER, i = it - row * PER;
+        char *drow = dst + row * pitch;
+        if (i >= NQ) {
+            *(u32x2 *)(drow + 2 * D + 8 * (i - NQ)) = u32x2{0u, 0u};
+            continue;
+        }
+        const bool valid = row < nvalid;
+        const int rr = valid ? row : 0;
+        const int64_t tok = (int64_t)tok0 + rr;
+        u32x2 r0, r1;
+        load_rotate_quad<D, E, FRA_DTYPE_F32, FULL>(x + rr * xs, p.cos + tok * p.sr_s * 4, p.sin + tok * p.sr_s * 4,
+                                                    i, valid, r0, r1);
+        *(u32x2 *)(drow + 8 * i) = r0;
+        *(u32x2 *)(drow + 2 * HALF + 8 * i) = r1;
+    }
+}
+
+// Rows [0, nrows) of x (row stride xs bytes) into LDS as 16-byte chunks,
+// zero past nvalid rows and past head_dim up to a multiple of 16.
+template <int D>
+__device__ __forceinline__ void stage_rows(char *dst, int pitch, const char *x, int64_t xs, int nvalid, int nrows,
+                                           int tid, int nthr) {
+    constexpr int CH = bwd_dp(D) / 8;
+    for (int it = tid; it < nrows * CH; it += nthr) {
+        const int row = it / CH, c = it - row * CH;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (row < nvalid && c < D / 8) v = *(const u32x4 *)(x + row * xs + 16 * c);
+        *(u32x4 *)(dst + row * pitch + 16 * c) = v;
+    }
+}
+
+// fp32 gradient rows of x_rot (LDS, `fpf` floats per row) -> gradient of x:
+// the transpose of the forward's rotation, x0r = x0 c0 - x1 s0,
+// x1r = x0 s1 + x1 c1 (c1 = c0, s1 = s0 for half-width tables), so
+// g0 = g0r c0 + g1r s1 and g1 = g1r c1 - g0r s0; rounded to the storage
+// dtype and stored to rows [0, nvalid) of dst (row stride ds bytes).
+template <int D, class E, bool FULL>
+__device__ __forceinline__ void unrotate_store(const float *f, int fpf, const BParams &p, char *dst, int64_t ds,
+                                               int tok0, int nvalid, int tid, int nthr) {
+    constexpr int NQ = D / 8, HALF = D / 2;
+    for (int it = tid; it < nvalid * NQ; it += nthr) {
+        const int row = it / NQ, i = it - row * NQ;
+        const f32x4 g0 = *(const f32x4 *)(f + row * fpf + 4 * i);
+        const f32x4 g1 = *(const f32x4 *)(f + row * fpf + HALF + 4 * i);
+        const int64_t tok = (int64_t)tok0 + row;
+        const char *crow = p.cos + tok * p.sr_s * 4, *srow = p.sin + tok * p.sr_s * 4;
+        const f32x4 c0 = *(const f32x4 *)(crow + 16 * i), s0 = *(const f32x4 *)(srow + 16 * i);
+        f32x4 c1 = c0, s1 = s0;
+        if constexpr (FULL) {
+            c1 = *(const f32x4 *)(crow + 4 * (HALF + 4 * i));
+            s1 = *(const f32x4 *)(srow + 4 * (HALF + 4 * i));
+        }
+        float x0[4], x1[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x0[e] = __builtin_fmaf(g0[e], c0[e], g1[e] * s1[e]);
+            x1[e] = __builtin_fmaf(g1[e], c1[e], -(g0[e] * s0[e]));
+        }
+        char *drow = dst + row * ds;
+        *(u32x2 *)(drow + 8 * i) = u32x2{E::pack(x0[0], x0[1]), E::pack(x0[2], x0[3])};
+        *(u32x2 *)(drow + 2 * HALF + 8 * i) = u32x2{E::pack(x1[0], x1[1]), E::pack(x1[2], x1[3])};
+    }
+}
+
+// Segment bounds of `seg`, clamped to [0, total] as in the forward.
+__device__ __forceinline__ void seg_bounds(const BParams &p, int seg, int &s0, int &L) {
+    int a = p.cu[seg], b = p.cu[seg + 1];
+    a = min(max(a, 0), p.total);
+    b = min(max(b, 0), p.total);
+    s0 = a;
+    L = b - a;
+}
+
+// Dvec[h, t] = sum_d dout[t, h, d] * out[t, h, d] in fp32, one thread per
+// (token, head) row.
+template <int D, class E>
+__global__ __launch_bounds__(256) void bwd_dot_kernel(const BParams p) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)p.total * p.num_heads) return;
+    const int t = (int)(i / p.num_heads), h = (int)(i - (int64_t)t * p.num_heads);
+    const char *o = p.out + ((int64_t)t * p.so_s + (int64_t)h * p.so_h) * 2;
+    const char *go = p.dout + ((int64_t)t * p.sdo_s + (int64_t)h * p.sdo_h) * 2;
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) {
+        const u32x4 a = *(const u32x4 *)(o + 16 * c), b = *(const u32x4 *)(go + 16 * c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            acc = __builtin_fmaf(E::lo(a[e]), E::lo(b[e]), acc);
+            acc = __builtin_fmaf(E::hi(a[e]), E::hi(b[e]), acc);
+        }
+    }
+    p.dvec[(int64_t)h * p.total + t] = acc;
+}
+
+// A operand of X^T B for a row-major LDS region X (pitch PITCH bytes) by
+// ds_read_b64_tr_b16, as in the forward's PV product: for k-step (a, h) of
+// 16 rows and d tile dt, lane (r, g) receives X[32a + 16h + {4g..4g+3,
+// 8+4g..8+4g+3}][32dt + r] -- the row order in which the accumulator layout
+// packs P / dZ as the B operand.
+template <int PITCH>
+__device__ __forceinline__ u32x4 tr_operand(const char *base, uint32_t lane_off, int a, int h, int dt) {
+    const char *cp = base + lane_off + (32 * a + 16 * h) * PITCH + 64 * dt;
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)cp);
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(cp + 8 * PITCH));
+    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+    return u32x4{l2[0], l2[1], h2[0], h2[1]};
+}
+
+template <int PITCH>
+__device__ __forceinline__ uint32_t tr_lane_offset(int lane) {
+    const int g = lane >> 5;
+    return (uint32_t)((4 * g + ((lane >> 2) & 3)) * PITCH + 2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
+}
+
+// Packs elements 8h..8h+7 of a 32x32 accumulator tile as a B operand.
+template <class E>
+__device__ __forceinline__ u32x4 pack8(const f32x16 &x, int h) {
+    return u32x4{E::pack(x[8 * h + 0], x[8 * h + 1]), E::pack(x[8 * h + 2], x[8 * h + 3]),
+                 E::pack(x[8 * h + 4], x[8 * h + 5]), E::pack(x[8 * h + 6], x[8 * h + 7])};
+}
+
+// ---- dq -------------------------------------------------------------------------
+
+template <int D, class E, bool FULL, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(BwdOcc<D>::kWaves, BwdOcc<D>::kWaves)))
+void bwd_dq_kernel(const BParams p) {
+    constexpr int DP = bwd_dp(D), S = DP / 16, NDT = (D + 31) / 32;
+    constexpr int PTR = bwd_pitch_tr(D), PRD = bwd_pitch_rows(D), FP = bwd_pitch_f32(D);
+    constexpr int BQ = 32 * NW, BKV = kBwdBlockKV, NT = 64 * NW;
+    constexpr int kKr = 0, kV = BKV * PTR;
+    constexpr int kStage = kV + BKV * PRD;
+    constexpr int kQ = BQ * PRD, kF = BQ * FP;
+    constexpr int kBytes = cmax(kStage, cmax(kQ, kF));
+    __shared__ __attribute__((aligned(16))) char lds[kBytes];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 31, g = lane >> 5;
+    const int unit = xcd_remap(blockIdx.x, gridDim.x);
+    const int sh = unit / p.blocks, qb = unit - sh * p.blocks;
+    const int seg = sh / p.num_heads, head = sh - seg * p.num_heads;
+    int s0, L;
+    seg_bounds(p, seg, s0, L);
+    const int q0 = qb * BQ;
+    if (q0 >= L) return;  // uniform
+    const int nq = min(BQ, L - q0);
+
+    // Q_rot of the block -> LDS -> the B operands of S^T (one query per lane).
+    stage_rotated<D, E, FULL>(lds, PRD, p, p.q + ((int64_t)(s0 + q0) * p.sq_s + (int64_t)head * p.sq_h) * 2,
+                              p.sq_s * 2, s0 + q0, nq, BQ, tid, NT);
+    __syncthreads();
+    const int qi = 32 * w + r;
+    const bool qvalid = qi < nq;
+    const int qrow = s0 + q0 + (qvalid ? qi : 0);
+    u32x4 qop[S], dop[S];
+    const char *dorow = p.dout + ((int64_t)qrow * p.sdo_s + (int64_t)head * p.sdo_h) * 2;
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+        qop[t] = *(const u32x4 *)(lds + qi * PRD + 32 * t + 16 * g);
+        const int d0 = 16 * t + 8 * g;
+        dop[t] = (qvalid && d0 < D) ? *(const u32x4 *)(dorow + 2 * d0) : u32x4{0u, 0u, 0u, 0u};
+    }
+    const int64_t srow = (int64_t)head * p.total + qrow;
+    const float lse2 = p.lse[srow] * kLog2e;
+    const float dvq = p.dvec[srow];
+    const float sl = p.scale_log2;
+
+    f32x16 dqacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = f32x16{};
+    const uint32_t trl = tr_lane_offset<PTR>(lane);
+    const int nkb = (L + BKV - 1) / BKV;
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int k0 = kb * BKV, nk = min(BKV, L - k0);
+        __syncthreads();  // the previous block's (or Q's) LDS reads are done
+        stage_rotated<D, E, FULL>(lds + kKr, PTR, p,
+                                  p.k + ((int64_t)(s0 + k0) * p.sk_s + (int64_t)head * p.sk_h) * 2, p.sk_s * 2,
+                                  s0 + k0, nk, BKV, tid, NT);
+        stage_rows<D>(lds + kV, PRD, p.v + ((int64_t)(s0 + k0) * p.sv_s + (int64_t)head * p.sv_h) * 2, p.sv_s * 2,
+                      nk, BKV, tid, NT);
+        __syncthreads();
+        // S^T = K_rot Q_rot^T and dP^T = V dout^T: rows key, column query.
+        f32x16 sacc[2], dpacc[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            sacc[a] = f32x16{};
+            dpacc[a] = f32x16{};
+#pragma unroll
+            for (int t = 0; t < S; ++t)
+                sacc[a] = E::mma(*(const u32x4 *)(lds + kKr + (32 * a + r) * PTR + 32 * t + 16 * g), qop[t], sacc[a]);
+#pragma unroll
+            for (int t = 0; t < S; ++t)
+                dpacc[a] = E::mma(*(const u32x4 *)(lds + kV + (32 * a + r) * PRD + 32 * t + 16 * g), dop[t], dpacc[a]);
+        }
+        // dZ^T = P^T * (dP^T - Dvec), keys past the segment masked.
+        u32x4 dsop[2][2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int key = 32 * a + 8 * (j >> 2) + 4 * g + (j & 3);
+                const float pj = key < nk ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[a][j], sl, -lse2)) : 0.f;
+                sacc[a][j] = pj * (dpacc[a][j] - dvq);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) dsop[a][h] = pack8<E>(sacc[a], h);
+        }
+        // dQ^T += K_rot^T dZ^T.
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+            for (int a = 0; a < 2; ++a) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    dqacc[dt] = E::mma(tr_operand<PTR>(lds + kKr, trl, a, h, dt), dsop[a][h], dqacc[dt]);
+            }
+        }
+    }
+
+    // dQ_rot rows (fp32, scaled) through LDS, then the inverse rotation.
+    __syncthreads();
+    float *f = (float *)lds;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+            const int d0 = 32 * dt + 8 * jq + 4 * g;
+            if (d0 < D)
+                *(f32x4 *)(f + qi * (FP / 4) + d0) =
+                    f32x4{dqacc[dt][4 * jq + 0], dqacc[dt][4 * jq + 1], dqacc[dt][4 * jq + 2], dqacc[dt][4 * jq + 3]} *
+                    p.scale;
+        }
+    }
+    __syncthreads();
+    unrotate_store<D, E, FULL>(f, FP / 4, p, p.dq + ((int64_t)(s0 + q0) * p.sdq_s + (int64_t)head * p.sdq_h) * 2,
+                               p.sdq_s * 2, s0 + q0, nq, tid, NT);
+}
+
+// ---- dk, dv -----------------------------------------------------------------------
+
+template <int D, class E, bool FULL, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(BwdOcc<D>::kWaves, BwdOcc<D>::kWaves)))
+void bwd_dkdv_kernel(const BParams p) {
+    constexpr int DP = bwd_dp(D), S = DP / 16, NDT = (D + 31) / 32;
+    constexpr int PTR = bwd_pitch_tr(D), PRD = bwd_pitch_rows(D), FP = bwd_pitch_f32(D);
+    constexpr int BKV = 32 * NW, BQ = kBwdBlockQ, NT = 64 * NW;
+    constexpr int kQr = 0, kDo = BQ * PTR, kLse = kDo + BQ * PTR, kDv = kLse + BQ * 4;
+    constexpr int kStage = kDv + BQ * 4;
+    constexpr int kK = BKV * PRD, kF = BKV * FP;
+    constexpr int kBytes = cmax(kStage, cmax(kK, kF));
+    __shared__ __attribute__((aligned(16))) char lds[kBytes];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 31, g = lane >> 5;
+    const int unit = xcd_remap(blockIdx.x, gridDim.x);
+    const int sh = unit / p.blocks, kb = unit - sh * p.blocks;
+    const int seg = sh / p.num_heads, head = sh - seg * p.num_heads;
+    int s0, L;
+    seg_bounds(p, seg, s0, L);
+    const int k0 = kb * BKV;
+    if (k0 >= L) return;  // uniform
+    const int nk = min(BKV, L - k0);
+
+    // K_rot and V of the block -> the B operands of S and dP (one key per lane).
+    stage_rotated<D, E, FULL>(lds, PRD, p, p.k + ((int64_t)(s0 + k0) * p.sk_s + (int64_t)head * p.sk_h) * 2,
+                              p.sk_s * 2, s0 + k0, nk, BKV, tid, NT);
+    __syncthreads();
+    const int ki = 32 * w + r;
+    const bool kvalid = ki < nk;
+    const int krow = s0 + k0 + (kvalid ? ki : 0);
+    u32x4 kop[S], vop[S];
+    const char *vrow = p.v + ((int64_t)krow * p.sv_s + (int64_t)head * p.sv_h) * 2;
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+        kop[t] = *(const u32x4 *)(lds + ki * PRD + 32 * t + 16 * g);
+        const int d0 = 16 * t + 8 * g;
+        vop[t] = (kvalid && d0 < D) ? *(const u32x4 *)(vrow + 2 * d0) : u32x4{0u, 0u, 0u, 0u};
+    }
+    const float sl = p.scale_log2;
+    f32x16 dvacc[NDT], dkacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+        dvacc[dt] = f32x16{};
+        dkacc[dt] = f32x16{};
+    }
+    const uint32_t trl = tr_lane_offset<PTR>(lane);
+    const float *lsef = (const float *)(lds + kLse);
+    const float *dvf = (const float *)(lds + kDv);
+    const int nqb = (L + BQ - 1) / BQ;
+    for (int qb = 0; qb < nqb; ++qb) {
+        const int q0 = qb * BQ, nq = min(BQ, L - q0);
+        __syncthreads();  // the previous block's (or K's) LDS reads are done
+        stage_rotated<D, E, FULL>(lds + kQr, PTR, p,
+                                  p.q + ((int64_t)(s0 + q0) * p.sq_s + (int64_t)head * p.sq_h) * 2, p.sq_s * 2,
+                                  s0 + q0, nq, BQ, tid, NT);
+        stage_rows<D>(lds + kDo, PTR, p.dout + ((int64_t)(s0 + q0) * p.sdo_s + (int64_t)head * p.sdo_h) * 2,
+                      p.sdo_s * 2, nq, BQ, tid, NT);
+        if (tid < BQ) {
+            // Rows past the segment: lse = +inf makes their P (and dZ) zero.
+            const int64_t srow = (int64_t)head * p.total + s0 + q0 + tid;
+            ((float *)(lds + kLse))[tid] = tid < nq ? p.lse[srow] * kLog2e : __builtin_inff();
+            ((float *)(lds + kDv))[tid] = tid < nq ? p.dvec[srow] : 0.f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            if (32 * a >= nq) break;  // uniform
+            // S = Q_rot K_rot^T and dP = dout V^T: rows query, column key.
+            f32x16 sacc = f32x16{}, dpacc = f32x16{};
+#pragma unroll
+            for (int t = 0; t < S; ++t)
+                sacc = E::mma(*(const u32x4 *)(lds + kQr + (32 * a + r) * PTR + 32 * t + 16 * g), kop[t], sacc);
+#pragma unroll
+            for (int t = 0; t < S; ++t)
+                dpacc = E::mma(*(const u32x4 *)(lds + kDo + (32 * a + r) * PTR + 32 * t + 16 * g), vop[t], dpacc);
+            // Element j holds query 32a + 8(j/4) + 4g + (j%4).
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const f32x4 l4 = *(const f32x4 *)(lsef + 32 * a + 8 * m + 4 * g);
+                const f32x4 d4 = *(const f32x4 *)(dvf + 32 * a + 8 * m + 4 * g);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int j = 4 * m + i;
+                    const float pj = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j], sl, -l4[i]));
+                    sacc[j] = pj;
+                    dpacc[j] = pj * (dpacc[j] - d4[i]);
+                }
+            }
+            u32x4 pop[2], dsop[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                pop[h] = pack8<E>(sacc, h);
+                dsop[h] = pack8<E>(dpacc, h);
+            }
+            // dV^T += dout^T P and dK^T += Q_rot^T dZ.
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    dvacc[dt] = E::mma(tr_operand<PTR>(lds + kDo, trl, a, h, dt), pop[h], dvacc[dt]);
+                    dkacc[dt] = E::mma(tr_operand<PTR>(lds + kQr, trl, a, h, dt), dsop[h], dkacc[dt]);
+                }
+            }
+        }
+    }
+
+    // dV rows straight from the accumulators (lane (r, g): key ki, d = 32dt +
+    // 8jq + 4g .. +3).
+    if (kvalid) {
+        char *dvr = p.dv + ((int64_t)(s0 + k0 + ki) * p.sdv_s + (int64_t)head * p.sdv_h) * 2;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq) {
+                const int d0 = 32 * dt + 8 * jq + 4 * g;
+                if (d0 < D)
+                    *(u32x2 *)(dvr + 2 * d0) = u32x2{E::pack(dvacc[dt][4 * jq + 0], dvacc[dt][4 * jq + 1]),
+                                                     E::pack(dvacc[dt][4 * jq + 2], dvacc[dt][4 * jq + 3])};
+            }
+        }
+    }
+    // dK_rot rows (fp32, scaled) through LDS, then the inverse rotation.
+    __syncthreads();
+    float *f = (float *)lds;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+            const int d0 = 32 * dt + 8 * jq + 4 * g;
+            if (d0 < D)
+                *(f32x4 *)(f + ki * (FP / 4) + d0) =
+                    f32x4{dkacc[dt][4 * jq + 0], dkacc[dt][4 * jq + 1], dkacc[dt][4 * jq + 2], dkacc[dt][4 * jq + 3]} *
+                    p.scale;
+        }
+    }
+    __syncthreads();
+    unrotate_store<D, E, FULL>(f, FP / 4, p, p.dk + ((int64_t)(s0 + k0) * p.sdk_s + (int64_t)head * p.sdk_h) * 2,
+                               p.sdk_s * 2, s0 + k0, nk, tid, NT);
+}
+
+// ---- host-side dispatch -------------------------------------------------------------
+
+typedef void (*BwdFn)(BParams);
+
+struct BwdKernels {
+    BwdFn dot, dq, dkdv;
+    int nw;
+};
+
+template <int D, class E, bool FULL, int NW>
+BwdKernels bwd_kernels_nw() {
+    return BwdKernels{(BwdFn)bwd_dot_kernel<D, E>, (BwdFn)bwd_dq_kernel<D, E, FULL, NW>,
+                      (BwdFn)bwd_dkdv_kernel<D, E, FULL, NW>, NW};
+}
+
+template <int D, class E, bool FULL>
+BwdKernels bwd_kernels_full(bool small) {
+    return small ? bwd_kernels_nw<D, E, FULL, 2>() : bwd_kernels_nw<D, E, FULL, 4>();
+}
+
+template <int D, class E>
+BwdKernels bwd_kernels_e(bool full, bool small) {
+    return full ? bwd_kernels_full<D, E, true>(small) : bwd_kernels_full<D, E, false>(small);
+}
+
+template <int D>
+BwdKernels bwd_kernels_d(int qkv, bool full, bool small) {
+    return qkv == FRA_DTYPE_BF16 ? bwd_kernels_e<D, BF16>(full, small) : bwd_kernels_e<D, F16>(full, small);
+}
+
+bool bwd_pick(int d, int qkv, bool full, bool small, BwdKernels &k) {
+    switch (d) {
+        case 64: k = bwd_kernels_d<64>(qkv, full, small); return true;
+        case 72: k = bwd_kernels_d<72>(qkv, full, small); return true;
+        case 80: k = bwd_kernels_d<80>(qkv, full, small); return true;
+        case 96: k = bwd_kernels_d<96>(qkv, full, small); return true;
+        case 128: k = bwd_kernels_d<128>(qkv, full, small); return true;
+        default: return false;
+    }
+}
+
+bool aligned_to(const void *ptr, int bytes) { return ((uintptr_t)ptr % (uintptr_t)bytes) == 0; }
+
+int64_t bwd_ws_bytes(const fra_bwd_args *a) { return (int64_t)a->num_heads * a->total_seq * 4; }
+
+int bwd_check(const fra_bwd_args *a) {
+    if (!a) return fra_fail(FRA_EINVAL, "args is NULL");
+    if (a->flags != 0) return fra_fail(FRA_EINVAL, "flags must be 0, got %d", a->flags);
+    if (a->num_heads <= 0) return fra_fail(FRA_EINVAL, "num_heads must be positive, got %d", a->num_heads);
+    if (a->head_dim <= 0 || a->head_dim % 2 != 0)
+        return fra_fail(FRA_EINVAL, "head_dim must be positive and even, got %d", a->head_dim);
+    if (a->total_seq < 0) return fra_fail(FRA_EINVAL, "total_seq must be >= 0, got %d", a->total_seq);
+    if (a->num_seqs < 1) return fra_fail(FRA_EINVAL, "num_seqs must be >= 1, got %d", a->num_seqs);
+    if (a->max_seqlen < 1) return fra_fail(FRA_EINVAL, "max_seqlen must be >= 1, got %d", a->max_seqlen);
+    if (a->qkv_dtype != FRA_DTYPE_BF16 && a->qkv_dtype != FRA_DTYPE_F16)
+        return fra_fail(FRA_EINVAL, "qkv_dtype must be bf16 or f16, got %d", a->qkv_dtype);
+    if (a->rope_dtype != FRA_DTYPE_F32 && a->rope_dtype != FRA_DTYPE_BF16 && a->rope_dtype != FRA_DTYPE_F16)
+        return fra_fail(FRA_EINVAL, "rope_dtype must be f32, bf16 or f16, got %d", a->rope_dtype);
+    const int d = a->head_dim;
+    if (a->rope_width != d / 2 && a->rope_width != d)
+        return fra_fail(FRA_EINVAL, "rope_width must be head_dim/2=%d or head_dim=%d, got %d", d / 2, d,
+                        a->rope_width);
+    if (!(a->softmax_scale > 0.f) || a->softmax_scale == __builtin_inff())
+        return fra_fail(FRA_EINVAL, "softmax_scale must be finite and > 0, got %g", (double)a->softmax_scale);
+    if (!a->q || !a->k || !a->v || !a->cos || !a->sin || !a->out || !a->dout || !a->lse || !a->cu_seqlens ||
+        !a->dq || !a->dk || !a->dv)
+        return fra_fail(FRA_EINVAL, "a tensor pointer is NULL");
+    const int64_t st[19] = {a->q_stride_seq,    a->q_stride_head,  a->k_stride_seq,    a->k_stride_head,
+                            a->v_stride_seq,    a->v_stride_head,  a->out_stride_seq,  a->out_stride_head,
+                            a->dout_stride_seq, a->dout_stride_head, a->dq_stride_seq, a->dq_stride_head,
+                            a->dk_stride_seq,   a->dk_stride_head, a->dv_stride_seq,   a->dv_stride_head,
+                            a->rope_stride_seq, 0, 0};
+    for (int i = 0; i < 17; ++i)
+        if (st[i] < 0) return fra_fail(FRA_EINVAL, "strides must be >= 0");
+    BwdKernels k;
+    if (!bwd_pick(d, a->qkv_dtype, a->rope_width == d, true, k))
+        return fra_fail(FRA_EUNSUPPORTED, "head_dim=%d has no compiled kernel (built: 64, 72, 80, 96, 128)", d);
+    if (a->rope_dtype != FRA_DTYPE_F32)
+        return fra_fail(FRA_EUNSUPPORTED, "the backward takes float32 cos/sin tables, got %s",
+                        a->rope_dtype == FRA_DTYPE_BF16 ? "bf16" : "f16");
+    const void *t16[8] = {a->q, a->k, a->v, a->out, a->dout, a->dq, a->dk, a->dv};
+    for (int i = 0; i < 8; ++i)
+        if (!aligned_to(t16[i], 16))
+            return fra_fail(FRA_EUNSUPPORTED, "q/k/v/out/dout/dq/dk/dv must be 16-byte aligned");
+    for (int i = 0; i < 16; ++i)
+        if (st[i] % 8)
+            return fra_fail(FRA_EUNSUPPORTED,
+                            "q/k/v/out/dout/dq/dk/dv strides must be multiples of 8 elements");
+    if (!aligned_to(a->cos, 16) || !aligned_to(a->sin, 16) || a->rope_stride_seq % 4)
+        return fra_fail(FRA_EUNSUPPORTED,
+                        "cos/sin must be 16-byte aligned with a row stride that is a multiple of 4 elements");
+    if (!aligned_to(a->lse, 4)) return fra_fail(FRA_EINVAL, "lse must be 4-byte aligned");
+    return FRA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fra_bwd_workspace_bytes(const fra_bwd_args *args, int64_t *bytes) {
+    if (!bytes) return fra_fail(FRA_EINVAL, "bytes is NULL");
+    *bytes = 0;
+    const int rc = bwd_check(args);
+    if (rc != FRA_OK) return rc;
+    *bytes = bwd_ws_bytes(args);
+    return fra_fail(FRA_OK, "%s", "");
+}
+
+int fra_bwd_varlen(const fra_bwd_args *a, void *stream) {
+    int rc = bwd_check(a);
+    if (rc != FRA_OK) return rc;
+    if (a->total_seq == 0) return fra_fail(FRA_OK, "%s", "");
+    if (!a->workspace || a->workspace_bytes < bwd_ws_bytes(a) || !aligned_to(a->workspace, 16))
+        return fra_fail(FRA_EINVAL, "workspace must be 16-byte aligned and hold at least %lld bytes",
+                        (long long)bwd_ws_bytes(a));
+    const int d = a->head_dim;
+    BwdKernels k;
+    bwd_pick(d, a->qkv_dtype, a->rope_width == d, a->max_seqlen <= 64, k);
+
+    BParams p;
+    memset(&p, 0, sizeof(p));
+    p.q = (const char *)a->q;
+    p.k = (const char *)a->k;
+    p.v = (const char *)a->v;
+    p.cos = (const char *)a->cos;
+    p.sin = (const char *)a->sin;
+    p.out = (const char *)a->out;
+    p.dout = (const char *)a->dout;
+    p.lse = a->lse;
+    p.cu = a->cu_seqlens;
+    p.dq = (char *)a->dq;
+    p.dk = (char *)a->dk;
+    p.dv = (char *)a->dv;
+    p.dvec = (float *)a->workspace;
+    p.sq_s = a->q_stride_seq;
+    p.sq_h = a->q_stride_head;
+    p.sk_s = a->k_stride_seq;
+    p.sk_h = a->k_stride_head;
+    p.sv_s = a->v_stride_seq;
+    p.sv_h = a->v_stride_head;
+    p.so_s = a->out_stride_seq;
+    p.so_h = a->out_stride_head;
+    p.sdo_s = a->dout_stride_seq;
+    p.sdo_h = a->dout_stride_head;
+    p.sdq_s = a->dq_stride_seq;
+    p.sdq_h = a->dq_stride_head;
+    p.sdk_s = a->dk_stride_seq;
+    p.sdk_h = a->dk_stride_head;
+    p.sdv_s = a->dv_stride_seq;
+    p.sdv_h = a->dv_stride_head;
+    p.sr_s = a->rope_stride_seq;
+    p.total = a->total_seq;
+    p.num_heads = a->num_heads;
+    p.num_seqs = a->num_seqs;
+    p.scale = a->softmax_scale;
+    p.scale_log2 = a->softmax_scale * kLog2e;
+
+    const hipStream_t st = (hipStream_t)stream;
+    const int64_t rows = (int64_t)a->total_seq * a->num_heads;
+    const int64_t sh = (int64_t)a->num_seqs * a->num_heads;
+    const int rows_per_wg = 32 * k.nw;
+    const int64_t blocks = (a->max_seqlen + rows_per_wg - 1) / rows_per_wg;
+    const int64_t grid_dot = (rows + 255) / 256, grid = sh * blocks;
+    if (grid_dot > 0x7fffffff || grid > 0x7fffffff)
+        return fra_fail(FRA_EUNSUPPORTED, "grid of %lld workgroups is too large", (long long)std::max(grid, grid_dot));
+    p.blocks = (int32_t)blocks;
+    hipLaunchKernelGGL(k.dot, dim3((unsigned)grid_dot), dim3(256), 0, st, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fra_fail(FRA_EHIP, "launch of the backward row dot products failed: %s", hipGetErrorString(e));
+    hipLaunchKernelGGL(k.dq, dim3((unsigned)grid), dim3(64 * k.nw), 0, st, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fra_fail(FRA_EHIP, "launch of the dq kernel failed: %s", hipGetErrorString(e));
+    hipLaunchKernelGGL(k.dkdv, dim3((unsigned)grid), dim3(64 * k.nw), 0, st, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fra_fail(FRA_EHIP, "launch of the dk/dv kernel failed: %s", hipGetErrorString(e));
+    return fra_fail(FRA_OK, "%s", "");
+}
+
+}  // extern "C"

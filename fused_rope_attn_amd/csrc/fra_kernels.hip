@@ -35,22 +35,9 @@
 #include <type_traits>
 
 #include "fra.h"
+#include "fra_device.h"
 
 namespace {
-
-typedef uint32_t u32;
-typedef uint16_t u16;
-typedef __attribute__((__vector_size__(2 * sizeof(u32)))) u32 u32x2;
-typedef __attribute__((__vector_size__(4 * sizeof(u32)))) u32 u32x4;
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
-typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
-typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
-typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
-typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
-typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2;
-
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kNegInf = -__builtin_inff();
 
 // Kernel parameters, passed by value.  Strides are in elements.
 struct KParams {
@@ -67,175 +54,8 @@ struct KParams {
     char *ws;
     int32_t dense_heads;  // window kernel: q, k, v and out have head stride == head_dim
     float scale_log2;     // softmax_scale * log2(e)
+    float *lse;           // optional [num_heads, total] natural-log row sums (NULL: not written)
 };
-
-// ---- element traits ---------------------------------------------------------
-
-struct BF16 {
-    static __device__ __forceinline__ float lo(u32 w) { return __builtin_bit_cast(float, w << 16); }
-    static __device__ __forceinline__ float hi(u32 w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
-    static __device__ __forceinline__ u32 pack(float a, float b) {
-        bf16x2 v = {(__bf16)a, (__bf16)b};  // v_cvt_pk_bf16_f32, round to nearest even
-        return __builtin_bit_cast(u32, v);
-    }
-    static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                      __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-    }
-};
-
-struct F16 {
-    static __device__ __forceinline__ float lo(u32 w) {
-        return (float)__builtin_bit_cast(_Float16, (u16)(w & 0xffffu));
-    }
-    static __device__ __forceinline__ float hi(u32 w) {
-        return (float)__builtin_bit_cast(_Float16, (u16)(w >> 16));
-    }
-    static __device__ __forceinline__ u32 pack(float a, float b) {
-        f16x2 v = {(_Float16)a, (_Float16)b};  // round to nearest even
-        return __builtin_bit_cast(u32, v);
-    }
-    static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                     __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-    }
-};
-
-// cos/sin table element types: a quad (4 consecutive entries) as fp32.
-template <int RD> struct Rope;
-template <> struct Rope<FRA_DTYPE_F32> {
-    static constexpr int kBytes = 4;
-    static __device__ __forceinline__ f32x4 quad(const char *p) { return *(const f32x4 *)p; }
-};
-template <> struct Rope<FRA_DTYPE_BF16> {
-    static constexpr int kBytes = 2;
-    static __device__ __forceinline__ f32x4 quad(const char *p) {
-        u32x2 w = *(const u32x2 *)p;
-        return f32x4{BF16::lo(w[0]), BF16::hi(w[0]), BF16::lo(w[1]), BF16::hi(w[1])};
-    }
-};
-template <> struct Rope<FRA_DTYPE_F16> {
-    static constexpr int kBytes = 2;
-    static __device__ __forceinline__ f32x4 quad(const char *p) {
-        u32x2 w = *(const u32x2 *)p;
-        return f32x4{F16::lo(w[0]), F16::hi(w[0]), F16::lo(w[1]), F16::hi(w[1])};
-    }
-};
-
-// ---- small helpers ------------------------------------------------------------
-
-// Consecutive logical units on the same XCD.  Workgroup b is dispatched to
-// XCD b % 8; this bijection on [0, n) gives XCD x the contiguous range of
-// units [x*ceil, ...), so units that share cache lines (adjacent heads of a
-// window, the query blocks of one head) share one L2.
-__device__ __forceinline__ int xcd_remap(int b, int n) {
-    constexpr int kXcd = 8;
-    const int xcd = b % kXcd, local = b / kXcd;
-    const int base = n / kXcd, rem = n % kXcd;
-    return xcd < rem ? xcd * (base + 1) + local : rem * (base + 1) + (xcd - rem) * base + local;
-}
-
-// v_permlane32_swap with both operands in a and b: lanes 32..63 of a trade
-// places with lanes 0..31 of b, so when both start as x, one of them holds
-// x of lanes 0..31 in both halves and the other x of lanes 32..63.  It is a
-// VALU op: no LDS round trip (and no wait on other LDS reads in flight) on
-// the softmax's critical path.  The clang builtin of this toolchain returns
-// the first register for both results, hence the asm; the s_nop gives the
-// two wait states a VALU write needs before the permlane reads it.
-__device__ __forceinline__ void permlane32_swap(float &a, float &b) {
-    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-
-// max and sum of x over lanes l and l ^ 32 (symmetric, so the result does
-// not depend on which operand receives which half).
-__device__ __forceinline__ float max_pair32(float x) {
-    float a = x, b = x;
-    permlane32_swap(a, b);
-    return fmaxf(a, b);
-}
-__device__ __forceinline__ float sum_pair32(float x) {
-    float a = x, b = x;
-    permlane32_swap(a, b);
-    return a + b;
-}
-
-// x of lane (l & 31) in every lane l: the upper half is zeroed first, so the
-// sum of the two swapped registers is the lower half's value whichever
-// register it lands in.
-__device__ __forceinline__ float bcast_lo32(float x) {
-    float a = (threadIdx.x & 32) ? 0.f : x, b = a;
-    permlane32_swap(a, b);
-    return a + b;
-}
-
-// max(a, b, c) in one instruction (the compiler only forms v_max3_f32 under
-// no-NaN assumptions, which the -inf masking rules out).
-__device__ __forceinline__ float max3f(float a, float b, float c) {
-    float d;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-    return d;
-}
-
-// An opaque copy of v: index arithmetic derived from it is recomputed in each
-// phase instead of being kept live (in registers) across the whole kernel.
-__device__ __forceinline__ int fresh(int v) {
-    asm volatile("" : "+v"(v));
-    return v;
-}
-
-__device__ __forceinline__ u32 perm(u32 hi_src, u32 lo_src, u32 sel) {
-    return __builtin_amdgcn_perm(hi_src, lo_src, sel);
-}
-constexpr u32 kSelLo = 0x05040100u;  // {lo16(lo_src), lo16(hi_src)}
-constexpr u32 kSelHi = 0x07060302u;  // {hi16(lo_src), hi16(hi_src)}
-
-// Split-half rotation of one quad pair in fp32 (reference
-// fused_attn.py:340-345 and :385-390: x0*cos - x1*sin, x0*sin + x1*cos),
-// packed to the storage dtype.  Each output is one product and one FMA, the
-// form FP contraction (on by default in Triton) gives the reference
-// expression; it differs from separately rounded products by at most one
-// fp32 rounding before the result is rounded to 16 bits.
-template <class E>
-__device__ __forceinline__ void rotate_quad(u32x2 x0w, u32x2 x1w, f32x4 c0, f32x4 s0, f32x4 c1, f32x4 s1,
-                                            u32x2 &r0w, u32x2 &r1w) {
-    const float x0[4] = {E::lo(x0w[0]), E::hi(x0w[0]), E::lo(x0w[1]), E::hi(x0w[1])};
-    const float x1[4] = {E::lo(x1w[0]), E::hi(x1w[0]), E::lo(x1w[1]), E::hi(x1w[1])};
-    float r0[4], r1[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        r0[i] = __builtin_fmaf(x0[i], c0[i], -(x1[i] * s0[i]));
-        r1[i] = __builtin_fmaf(x0[i], s1[i], x1[i] * c1[i]);
-    }
-    r0w = u32x2{E::pack(r0[0], r0[1]), E::pack(r0[2], r0[3])};
-    r1w = u32x2{E::pack(r1[0], r1[1]), E::pack(r1[2], r1[3])};
-}
-
-// Loads quad i (entries 4i..4i+3) of both halves of one x row and of the
-// matching cos/sin rows, and rotates it.  The loads are unconditional -- the
-// caller passes pointers that are valid for every lane (rows clamped into the
-// segment) -- so the load stream stays one straight-line block; `valid` false
-// zeroes the result.  FULL selects tables of width D (second half used for
-// x1', the HF layout) over width D/2 (the reference layout).
-template <int D, class E, int RD, bool FULL>
-__device__ __forceinline__ void load_rotate_quad(const char *xrow, const char *crow, const char *srow, int i,
-                                                 bool valid, u32x2 &r0w, u32x2 &r1w) {
-    constexpr int HALF = D / 2;
-    constexpr int RB = Rope<RD>::kBytes;
-    u32x2 x0 = *(const u32x2 *)(xrow + 8 * i);
-    u32x2 x1 = *(const u32x2 *)(xrow + 2 * HALF + 8 * i);
-    const f32x4 c0 = Rope<RD>::quad(crow + RB * 4 * i);
-    const f32x4 s0 = Rope<RD>::quad(srow + RB * 4 * i);
-    f32x4 c1 = c0, s1 = s0;
-    if constexpr (FULL) {
-        c1 = Rope<RD>::quad(crow + RB * (HALF + 4 * i));
-        s1 = Rope<RD>::quad(srow + RB * (HALF + 4 * i));
-    }
-    if (!valid) {
-        x0 = u32x2{0u, 0u};
-        x1 = u32x2{0u, 0u};
-    }
-    rotate_quad<E>(x0, x1, c0, s0, c1, s1, r0w, r1w);
-}
 
 // ---- window kernel ------------------------------------------------------------
 //
@@ -577,7 +397,7 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
         (uint32_t)((4 * g + ((lane >> 2) & 3)) * VP + 2 * (w * D + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
     // Output quad i of a tile: d0 = 32 (i / 4) + 8 (i % 4) + 4g.  Quads past
     // OQV (d0 >= D for both g) are not kept; quad OQV - 1 may be half valid.
-    auto tile = [&](const u32x4 (&qcur)[S], u32x2 (&outq)[OQV]) {
+    auto tile = [&](const u32x4 (&qcur)[S], u32x2 (&outq)[OQV], int b) {
         // S^T tiles: rows kv, columns q.  Lane (r, g) holds q = 32b + r and
         // kv = 32a + 8(j/4) + 4g + (j%4) in element j of sacc[a].
         f32x16 sacc[2];
@@ -622,6 +442,8 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
         }
         lsum = sum_pair32(lsum);
         const float inv = 1.0f / lsum;
+        if (p.lse != nullptr && g == 0 && 32 * b + r < L)
+            p.lse[(int64_t)(h0 + w) * p.total + s0 + 32 * b + r] = (__builtin_amdgcn_logf(lsum) - mneg) * kLn2;
 
         // P^T as the B operand of O^T = V^T P^T: step (a, h) uses elements
         // 8h..8h+7 of sacc[a], i.e. kv = 32a + 16h + {4g..4g+3, 8+4g..8+4g+3}.
@@ -662,9 +484,9 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
     };
     u32x2 out0[OQV], out1[OQV];
     if (active) {  // uniform within the wavefront; no barrier inside
-        tile(qop[0], out0);
+        tile(qop[0], out0, 0);
         __builtin_amdgcn_sched_barrier(0);
-        if (L > 32) tile(qop[1], out1);
+        if (L > 32) tile(qop[1], out1, 1);
     }
     __syncthreads();  // V is dead: the output rows go over it
 
@@ -890,6 +712,7 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const KParams p) {
         }
     }
     const float inv = 1.0f / l;
+    if (p.lse != nullptr && c == 0) p.lse[(int64_t)head * p.total + s0 + q] = (mx + __builtin_amdgcn_logf(l)) * kLn2;
     char *orow = p.out + ((int64_t)(s0 + q) * p.so_s + (int64_t)head * p.so_h) * 2;
     *(u32x2 *)(orow + 8 * c) = u32x2{E::pack(acc[0] * inv, acc[1] * inv), E::pack(acc[2] * inv, acc[3] * inv)};
 }
@@ -1384,6 +1207,8 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     }
     if (q < L) {
         const float inv = 1.0f / l_i;
+        if (p.lse != nullptr && g == 0)
+            p.lse[(int64_t)head * p.total + s0 + q] = (m_i + __builtin_amdgcn_logf(l_i)) * kLn2;
         char *orow = p.out + ((int64_t)(s0 + q) * p.so_s + (int64_t)head * p.so_h) * 2;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
@@ -1634,6 +1459,8 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
     kp.num_seqs = a->num_seqs;
     kp.max_seqlen = a->max_seqlen;
     kp.scale_log2 = a->softmax_scale * kLog2e;
+    kp.lse = a->lse;
+    if (a->lse && !aligned(a->lse, 4)) return fail(FRA_EINVAL, "lse must be 4-byte aligned");
 
     const int64_t sh = (int64_t)a->num_seqs * a->num_heads;
     int64_t grid;
@@ -1688,6 +1515,14 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
 }
 
 }  // namespace
+
+int fra_fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
 
 extern "C" {
 
@@ -1763,5 +1598,7 @@ int32_t fra_abi_version(void) { return FRA_ABI_VERSION; }
 int32_t fra_sizeof_args(void) { return (int32_t)sizeof(fra_fwd_args); }
 
 int32_t fra_sizeof_plan(void) { return (int32_t)sizeof(fra_plan); }
+
+int32_t fra_sizeof_bwd_args(void) { return (int32_t)sizeof(fra_bwd_args); }
 
 }  // extern "C"

@@ -10,6 +10,11 @@ Drop-in for the reference module ``fused_attn.py``:
 * ``compute_rope_2d`` -- reference ``fused_attn.py:33-136`` (with its LRU
   cache, ``:18-30``): the cos/sin tables the op consumes.
 * ``next_pow2`` -- reference ``fused_attn.py:13-15``.
+
+Beyond the reference (which is forward-only): ``fused_rope_attention``
+records an autograd graph when q, k or v require grad, and
+``fused_rope_attention_fwd`` / ``fused_rope_attention_bwd`` expose the
+forward with its log-sum-exp and the gradients as plain functions.
 """
 import ctypes
 from collections import OrderedDict
@@ -18,7 +23,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["fused_rope_attention", "compute_rope_2d", "next_pow2", "plan"]
+__all__ = ["fused_rope_attention", "fused_rope_attention_fwd", "fused_rope_attention_bwd",
+           "compute_rope_2d", "next_pow2", "plan"]
 
 
 def next_pow2(n: int) -> int:
@@ -286,21 +292,34 @@ def fused_rope_attention(
     """
     _validate(q, k, v, cos, sin, cu_seqlens, out)
     cu = _prepare_cu(cu_seqlens, q.device)
-
-    if out is None:
-        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-
     if max_seqlen is None:
         max_seqlen = int((cu[1:] - cu[:-1]).max().item())
     max_seqlen = int(max_seqlen)
+    scale = q.shape[2] ** -0.5 if softmax_scale is None else float(softmax_scale)
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        if out is not None:
+            raise RuntimeError("fused_rope_attention(): out= does not support automatic differentiation "
+                               "(q, k or v requires grad)")
+        return _FusedRopeAttention.apply(q, k, v, cos, sin, cu, max_seqlen, scale)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    return _forward(q, k, v, cos, sin, cu, max_seqlen, scale, out, None)
+
+
+def _forward(q, k, v, cos, sin, cu, max_seqlen: int, scale: float, out, lse):
+    """One forward launch into ``out`` (and ``lse`` if given, [heads, tokens]
+    fp32); inputs already validated, ``cu`` int32 on q's device."""
     if max_seqlen <= 0 or q.shape[0] == 0:
+        if lse is not None:
+            lse.fill_(float("-inf"))
         return out.zero_()
     qk, kk, vk, cosk, sink = _prepare(q, k, v, cos, sin, _uses_long_kernel(max_seqlen, q.shape[2]))
     dst = out if _fits(out, 8, 4) else torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    scale = q.shape[2] ** -0.5 if softmax_scale is None else float(softmax_scale)
 
     lib = _lib.load()
     args = _build_args(qk, kk, vk, cosk, sink, dst, cu, max_seqlen, scale)
+    if lse is not None:
+        args.lse = lse.data_ptr()
     ws = None
     with torch.cuda.device(q.device):
         # The long kernel splits a partly filled last round of workgroups
@@ -316,3 +335,115 @@ def fused_rope_attention(
     if dst is not out:
         out.copy_(dst)
     return out
+
+
+def fused_rope_attention_fwd(q, k, v, cos, sin, cu_seqlens, max_seqlen=None, softmax_scale=None, *, out=None):
+    """Forward with the softmax statistics: returns ``(out, lse)``, where
+    ``lse[h, t] = log(sum_j exp(softmax_scale * q_rot[t, h] . k_rot[j, h]))``
+    over the keys of t's segment (float32, ``[num_heads, total_seq]``; the
+    natural-log convention of flash-attn's varlen ``softmax_lse``).  Entries
+    of rows outside every segment are unspecified.  No counterpart in the
+    reference, which keeps these statistics in registers
+    (fused_attn.py:347-355, 398-405)."""
+    _validate(q, k, v, cos, sin, cu_seqlens, out)
+    cu = _prepare_cu(cu_seqlens, q.device)
+    if max_seqlen is None:
+        max_seqlen = int((cu[1:] - cu[:-1]).max().item())
+    scale = q.shape[2] ** -0.5 if softmax_scale is None else float(softmax_scale)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
+    _forward(q, k, v, cos, sin, cu, int(max_seqlen), scale, out, lse)
+    return out, lse
+
+
+def _bwd_layout(t: torch.Tensor) -> torch.Tensor:
+    return _kernel_layout(t, 16, 8)
+
+
+def _backward(dout, q, k, v, cos, sin, out, lse, cu, max_seqlen: int, scale: float, dq, dk, dv):
+    """One backward launch (``fra_bwd_varlen``) writing dq, dk, dv."""
+    if max_seqlen <= 0 or q.shape[0] == 0:
+        return dq, dk, dv
+    lib = _lib.load()
+    q2, k2, v2, o2, do2 = (_bwd_layout(t) for t in (q, k, v, out, dout))
+    # The backward reads float32 tables (widening is exact).
+    cos2 = cos.float().contiguous()
+    sin2 = sin.float().contiguous()
+    lse2 = lse.contiguous()
+    dsts = [t if _fits(t, 16, 8) else torch.empty(q.shape, dtype=q.dtype, device=q.device) for t in (dq, dk, dv)]
+    a = _lib.BwdArgs()
+    for name, t in (("q", q2), ("k", k2), ("v", v2), ("out", o2), ("dout", do2),
+                    ("dq", dsts[0]), ("dk", dsts[1]), ("dv", dsts[2])):
+        setattr(a, name, t.data_ptr())
+        setattr(a, f"{name}_stride_seq", t.stride(0))
+        setattr(a, f"{name}_stride_head", t.stride(1))
+    a.cos, a.sin, a.lse, a.cu_seqlens = cos2.data_ptr(), sin2.data_ptr(), lse2.data_ptr(), cu.data_ptr()
+    a.rope_stride_seq = cos2.stride(0)
+    a.total_seq, a.num_heads, a.head_dim = q.shape
+    a.num_seqs = cu.numel() - 1
+    a.max_seqlen = int(max_seqlen)
+    a.rope_width = cos2.shape[1]
+    a.qkv_dtype = _QKV_CODE[q.dtype]
+    a.rope_dtype = _lib.FRA_DTYPE_F32
+    a.softmax_scale = float(scale)
+    a.flags = 0
+    with torch.cuda.device(q.device):
+        nbytes = ctypes.c_int64(0)
+        _lib.check(lib.fra_bwd_workspace_bytes(a, ctypes.byref(nbytes)))
+        ws = torch.empty(max(int(nbytes.value), 16), dtype=torch.uint8, device=q.device)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        _lib.check(lib.fra_bwd_varlen(a, torch.cuda.current_stream(q.device).cuda_stream))
+    for dst, t in zip(dsts, (dq, dk, dv)):
+        if dst is not t:
+            t.copy_(dst)
+    return dq, dk, dv
+
+
+def fused_rope_attention_bwd(dout, q, k, v, cos, sin, out, lse, cu_seqlens, max_seqlen=None, softmax_scale=None,
+                             *, dq=None, dk=None, dv=None):
+    """Gradients ``(dq, dk, dv)`` of ``fused_rope_attention`` given ``dout``
+    and the forward's ``out`` and ``lse`` (from ``fused_rope_attention_fwd``
+    with the same inputs).  cos/sin get no gradient.  Rows outside every
+    segment of freshly allocated results are zero.  No counterpart in the
+    reference (forward-only); the arithmetic is the derivative of its kernel
+    (fused_attn.py:316-423), with the rotation's rounding taken as the
+    identity."""
+    _validate(q, k, v, cos, sin, cu_seqlens, out)
+    if dout.shape != q.shape or dout.dtype != q.dtype or dout.device != q.device:
+        raise ValueError(f"dout must match q shape/dtype/device, got {tuple(dout.shape)} {dout.dtype} {dout.device}")
+    if lse.shape != (q.shape[1], q.shape[0]) or lse.dtype != torch.float32:
+        raise ValueError(f"lse must be float32 [num_heads, total_seq]={q.shape[1], q.shape[0]}, "
+                         f"got {tuple(lse.shape)} {lse.dtype}")
+    cu = _prepare_cu(cu_seqlens, q.device)
+    if max_seqlen is None:
+        max_seqlen = int((cu[1:] - cu[:-1]).max().item())
+    scale = q.shape[2] ** -0.5 if softmax_scale is None else float(softmax_scale)
+    dq = torch.zeros_like(q, memory_format=torch.contiguous_format) if dq is None else dq
+    dk = torch.zeros_like(k, memory_format=torch.contiguous_format) if dk is None else dk
+    dv = torch.zeros_like(v, memory_format=torch.contiguous_format) if dv is None else dv
+    return _backward(dout, q, k, v, cos, sin, out, lse, cu, int(max_seqlen), scale, dq, dk, dv)
+
+
+class _FusedRopeAttention(torch.autograd.Function):
+    """Autograd node of the op: the forward also writes the log-sum-exp, the
+    backward runs ``fra_bwd_varlen``.  cos/sin and cu_seqlens get no
+    gradient."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, cos, sin, cu, max_seqlen, scale):
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
+        _forward(q, k, v, cos, sin, cu, max_seqlen, scale, out, lse)
+        ctx.save_for_backward(q, k, v, cos, sin, out, lse, cu)
+        ctx.max_seqlen, ctx.scale = max_seqlen, scale
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, cos, sin, out, lse, cu = ctx.saved_tensors
+        dq = torch.zeros(q.shape, dtype=q.dtype, device=q.device)
+        dk = torch.zeros(q.shape, dtype=q.dtype, device=q.device)
+        dv = torch.zeros(q.shape, dtype=q.dtype, device=q.device)
+        _backward(dout, q, k, v, cos, sin, out, lse, cu, ctx.max_seqlen, ctx.scale, dq, dk, dv)
+        return dq, dk, dv, None, None, None, None, None

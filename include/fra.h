@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define FRA_ABI_VERSION 2
+#define FRA_ABI_VERSION 3
 
 /* Element types. */
 enum fra_dtype {
@@ -99,6 +99,15 @@ typedef struct fra_fwd_args {
      */
     void *workspace;
     int64_t workspace_bytes;
+    /*
+     * Optional output (no counterpart in the reference, whose kernel keeps
+     * the softmax statistics in registers): the natural-log row sums
+     * lse[h * total_seq + t] = log(sum_j exp(softmax_scale * q_rot[t,h] .
+     * k_rot[j,h])) over the keys j of t's segment, fp32, [num_heads,
+     * total_seq] contiguous, 4-byte aligned.  fra_bwd_varlen() consumes it.
+     * Entries of rows outside every segment are not written.  NULL: none.
+     */
+    float *lse;
 } fra_fwd_args;
 
 /* What fra_fwd_varlen() would launch for a set of arguments. */
@@ -147,6 +156,67 @@ int fra_query_plan(const fra_fwd_args *args, fra_plan *plan);
  */
 int fra_workspace_bytes(const fra_fwd_args *args, int64_t *bytes);
 
+/*
+ * Arguments of one backward call (no counterpart in the reference, which is
+ * forward-only; this is the training side of the same op).  Given dout =
+ * dL/dout of a forward call with the same q, k, v, cos, sin, cu_seqlens,
+ * max_seqlen and softmax_scale, and that call's out and lse, it writes
+ * dq, dk, dv = dL/dq, dL/dk, dL/dv.  cos and sin get no gradient.
+ * Every [total_seq, num_heads, head_dim] tensor (q, k, v, out, dout, dq,
+ * dk, dv) is 16-byte aligned with strides that are multiples of 8 elements;
+ * cos/sin are aligned to 4 of their elements with a row stride that is a
+ * multiple of 4 elements.  Rows outside every segment are not written.
+ */
+typedef struct fra_bwd_args {
+    const void *q;
+    const void *k;
+    const void *v;
+    const void *cos;
+    const void *sin;
+    const void *out;            /* the forward's output */
+    const void *dout;           /* gradient of the output, qkv_dtype */
+    const float *lse;           /* the forward's lse, [num_heads, total_seq] */
+    const int32_t *cu_seqlens;
+    void *dq;                   /* outputs, qkv_dtype */
+    void *dk;
+    void *dv;
+    int64_t q_stride_seq, q_stride_head;
+    int64_t k_stride_seq, k_stride_head;
+    int64_t v_stride_seq, v_stride_head;
+    int64_t out_stride_seq, out_stride_head;
+    int64_t dout_stride_seq, dout_stride_head;
+    int64_t dq_stride_seq, dq_stride_head;
+    int64_t dk_stride_seq, dk_stride_head;
+    int64_t dv_stride_seq, dv_stride_head;
+    int64_t rope_stride_seq;
+    int32_t total_seq;
+    int32_t num_heads;
+    int32_t head_dim;
+    int32_t num_seqs;
+    int32_t max_seqlen;
+    int32_t rope_width;
+    int32_t qkv_dtype;
+    int32_t rope_dtype;
+    float softmax_scale;
+    int32_t flags;              /* reserved, must be 0 */
+    /* Required device scratch of at least fra_bwd_workspace_bytes() bytes
+     * (the per-row dot products of dout and out); 16-byte aligned. */
+    void *workspace;
+    int64_t workspace_bytes;
+} fra_bwd_args;
+
+/*
+ * Gradients of fra_fwd_varlen() (see fra_bwd_args).  Three kernels on
+ * `stream`: the row dot products of dout and out, then dq (one workgroup per
+ * block of queries, looping over the keys of its segment) and dk, dv (one
+ * workgroup per block of keys, looping over the queries).  No atomics: the
+ * result is deterministic.  Returns FRA_OK or a negative enum fra_status.
+ */
+int fra_bwd_varlen(const fra_bwd_args *args, void *stream);
+
+/* Workspace bytes fra_bwd_varlen() needs for these arguments. */
+int fra_bwd_workspace_bytes(const fra_bwd_args *args, int64_t *bytes);
+
 /* 1 if head_dim has a compiled kernel in this build, else 0. */
 int fra_supports_head_dim(int32_t head_dim);
 
@@ -159,9 +229,11 @@ const char *fra_version(void);
 /* FRA_ABI_VERSION of the built library. */
 int32_t fra_abi_version(void);
 
-/* sizeof(fra_fwd_args) / sizeof(fra_plan) as compiled, for FFI checks. */
+/* sizeof(fra_fwd_args) / sizeof(fra_plan) / sizeof(fra_bwd_args) as
+ * compiled, for FFI checks. */
 int32_t fra_sizeof_args(void);
 int32_t fra_sizeof_plan(void);
+int32_t fra_sizeof_bwd_args(void);
 
 #ifdef __cplusplus
 }

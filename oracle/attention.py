@@ -200,3 +200,101 @@ def brute_force_f64(q, k, v, cos, sin, cu_seqlens, softmax_scale=None):
                     out[i, hh, j] = sum(w[t] * v[a + t, hh, j] for t in range(b - a)) / z
     return out
 
+
+
+# ---------------------------------------------------------------------------
+# Softmax statistics and gradients (beyond the reference, which is
+# forward-only: these restate the derivative of its arithmetic,
+# fused_attn.py:316-423, for the build's backward).
+# ---------------------------------------------------------------------------
+
+
+def rotate_transpose(g: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """Transpose of ``rotate`` applied to a gradient ``g [N, H, D]``: with
+    ``x0' = x0 c0 - x1 s0`` and ``x1' = x0 s1 + x1 c1`` (``c1 = c0``,
+    ``s1 = s0`` for half-width tables), ``g0 = g0' c0 + g1' s1`` and
+    ``g1 = g1' c1 - g0' s0``."""
+    g = np.asarray(g, dtype=np.float32)
+    d = g.shape[-1]
+    half = d // 2
+    cos = np.asarray(cos, dtype=np.float32)
+    sin = np.asarray(sin, dtype=np.float32)
+    c0, s0 = cos[:, None, :half], sin[:, None, :half]
+    if cos.shape[-1] == d:
+        c1, s1 = cos[:, None, half:], sin[:, None, half:]
+    else:
+        c1, s1 = c0, s0
+    g0, g1 = g[..., :half], g[..., half:]
+    return np.concatenate([g0 * c0 + g1 * s1, g1 * c1 - g0 * s0], axis=-1).astype(np.float32)
+
+
+def softmax_lse(q, k, cos, sin, cu_seqlens, softmax_scale=None) -> np.ndarray:
+    """Natural-log row sums ``lse[h, t] = log sum_j exp(scale * q_rot[t, h] .
+    k_rot[j, h])`` over the keys of t's segment, ``[H, N]`` fp32, NaN for rows
+    outside every segment (computed in float64)."""
+    q = np.asarray(q, dtype=np.float32)
+    n, h, d = q.shape
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(d)
+    qr = rotate(q, cos, sin).astype(np.float64)
+    kr = rotate(np.asarray(k, dtype=np.float32), cos, sin).astype(np.float64)
+    out = np.full((h, n), np.nan, dtype=np.float64)
+    for a, b in segments(cu_seqlens, n):
+        for hh in range(h):
+            s = (qr[a:b, hh] @ kr[a:b, hh].T) * softmax_scale
+            m = s.max(axis=-1, keepdims=True)
+            out[hh, a:b] = (m + np.log(np.exp(s - m).sum(axis=-1, keepdims=True)))[:, 0]
+    return out.astype(np.float32)
+
+
+def fused_rope_attention_bwd(dout, q, k, v, cos, sin, cu_seqlens, softmax_scale=None, mode: str = "fp32"):
+    """Gradients ``(dq, dk, dv)`` of the oracle's forward at ``dout``.
+
+    Per segment and head, with ``P = softmax(scale * q_rot k_rot^T)`` and
+    ``O = P v``: ``dv = P^T dout``, ``dZ = P * (dout v^T - rowsum(dout * O))``,
+    ``dq = rot^T(scale * dZ k_rot)``, ``dk = rot^T(scale * dZ^T q_rot)``.
+
+    ``mode="fp32"``: all in fp32 from the inputs (the parity target).
+    ``mode="bf16"``/``"f16"``: diagnostic model of the GPU kernels' rounding
+    points: q_rot/k_rot rounded to the dtype, O rounded (the forward's
+    output), P and dZ rounded before their products, results rounded.
+    Rows outside every segment are NaN.
+    """
+    dout = np.asarray(dout, dtype=np.float32)
+    q = np.asarray(q, dtype=np.float32)
+    k = np.asarray(k, dtype=np.float32)
+    v = np.asarray(v, dtype=np.float32)
+    n, h, d = q.shape
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(d)
+    scale = np.float32(softmax_scale)
+    emulate = mode in ("bf16", "f16")
+    if mode not in ("fp32", "bf16", "f16"):
+        raise ValueError(f"unknown mode {mode!r}")
+    rnd = (lambda x: round_to(x, mode)) if emulate else (lambda x: x)
+    qr = rnd(rotate(q, cos, sin))
+    kr = rnd(rotate(k, cos, sin))
+    dqr = np.full((n, h, d), np.nan, dtype=np.float32)
+    dkr = np.full((n, h, d), np.nan, dtype=np.float32)
+    dv = np.full((n, h, d), np.nan, dtype=np.float32)
+    for a, b in segments(cu_seqlens, n):
+        for hh in range(h):
+            qs, ks, vs, gs = qr[a:b, hh], kr[a:b, hh], v[a:b, hh], dout[a:b, hh]
+            s = (qs @ ks.T) * scale
+            p = _softmax_rows(s).astype(np.float32)
+            o = rnd((p @ vs).astype(np.float32)) if not emulate else rnd(
+                (round_to(p, mode) @ vs).astype(np.float32))
+            dvec = (gs * o).sum(axis=-1, keepdims=True, dtype=np.float32)
+            dp = (gs @ vs.T).astype(np.float32)
+            dz = (p * (dp - dvec)).astype(np.float32)
+            dv[a:b, hh] = rnd(p).T @ gs
+            dqr[a:b, hh] = (rnd(dz) @ ks) * scale
+            dkr[a:b, hh] = (rnd(dz).T @ qs) * scale
+    dq = rotate_transpose(dqr, cos, sin)
+    dk = rotate_transpose(dkr, cos, sin)
+    if emulate:
+        covered = ~np.isnan(dq)
+        dq[covered] = round_to(dq[covered], mode)
+        dk[covered] = round_to(dk[covered], mode)
+        dv[covered] = round_to(dv[covered], mode)
+    return dq, dk, dv

@@ -134,3 +134,75 @@ def test_null_args_and_empty_problem():
     # total_seq == 0 validates and returns without launching
     assert lib.fra_fwd_varlen(make_args(n=0), None) == _lib.FRA_OK
     assert lib.fra_last_error() == b""
+
+
+def test_forward_lse_pointer_alignment():
+    lib = _lib.load()
+    a = make_args(lse=(1 << 20) * 9 + 2)
+    assert lib.fra_fwd_varlen(a, None) == _lib.FRA_EINVAL
+    assert "lse" in lib.fra_last_error().decode()
+
+
+def make_bwd_args(**kw):
+    a = _lib.BwdArgs()
+    n, h, d = kw.get("n", 1024), kw.get("h", 16), kw.get("d", 80)
+    base = 1 << 20  # fake, aligned device addresses: nothing is launched
+    names = ("q", "k", "v", "cos", "sin", "out", "dout", "lse", "cu_seqlens", "dq", "dk", "dv")
+    for i, name in enumerate(names):
+        setattr(a, name, base * (i + 1))
+    for t in ("q", "k", "v", "out", "dout", "dq", "dk", "dv"):
+        setattr(a, f"{t}_stride_seq", h * d)
+        setattr(a, f"{t}_stride_head", d)
+    a.rope_stride_seq = d // 2
+    a.total_seq, a.num_heads, a.head_dim = n, h, d
+    a.num_seqs = kw.get("nseg", 16)
+    a.max_seqlen = kw.get("max_seqlen", 64)
+    a.rope_width = d // 2
+    a.qkv_dtype, a.rope_dtype = _lib.FRA_DTYPE_BF16, _lib.FRA_DTYPE_F32
+    a.softmax_scale = d ** -0.5
+    a.flags = 0
+    for key, val in kw.items():
+        if key not in ("n", "h", "d", "nseg"):
+            setattr(a, key, val)
+    return a
+
+
+def test_bwd_struct_and_workspace_size():
+    lib = _lib.load()
+    assert lib.fra_sizeof_bwd_args() == ctypes.sizeof(_lib.BwdArgs)
+    nbytes = ctypes.c_int64(-1)
+    assert lib.fra_bwd_workspace_bytes(make_bwd_args(n=9216, h=16), ctypes.byref(nbytes)) == _lib.FRA_OK
+    assert nbytes.value == 9216 * 16 * 4  # one fp32 per (head, token): the rows' dout . out
+    # total_seq == 0 validates and returns without launching (no workspace needed)
+    assert lib.fra_bwd_varlen(make_bwd_args(n=0), None) == _lib.FRA_OK
+
+
+@pytest.mark.parametrize("field,value,code,msg", [
+    ("dout", 0, _lib.FRA_EINVAL, "NULL"),
+    ("lse", 0, _lib.FRA_EINVAL, "NULL"),
+    ("dk", 0, _lib.FRA_EINVAL, "NULL"),
+    ("d", 88, _lib.FRA_EUNSUPPORTED, "head_dim"),
+    ("rope_dtype", _lib.FRA_DTYPE_BF16, _lib.FRA_EUNSUPPORTED, "float32"),
+    ("dq", (1 << 20) * 10 + 8, _lib.FRA_EUNSUPPORTED, "16-byte aligned"),
+    ("dout_stride_head", 84, _lib.FRA_EUNSUPPORTED, "multiples of 8"),
+    ("cos", (1 << 20) * 4 + 8, _lib.FRA_EUNSUPPORTED, "cos/sin"),
+    ("lse", (1 << 20) * 8 + 2, _lib.FRA_EINVAL, "lse"),
+    ("flags", 2, _lib.FRA_EINVAL, "flags"),
+    ("max_seqlen", 0, _lib.FRA_EINVAL, "max_seqlen"),
+])
+def test_bwd_validation_errors(field, value, code, msg):
+    lib = _lib.load()
+    a = make_bwd_args(**{field: value})
+    nbytes = ctypes.c_int64(0)
+    assert lib.fra_bwd_workspace_bytes(a, ctypes.byref(nbytes)) == code
+    assert msg in lib.fra_last_error().decode()
+    assert lib.fra_bwd_varlen(a, None) == code  # fails before any launch
+
+
+def test_bwd_requires_workspace():
+    lib = _lib.load()
+    a = make_bwd_args()
+    assert lib.fra_bwd_varlen(a, None) == _lib.FRA_EINVAL  # no workspace: fails before any launch
+    assert "workspace" in lib.fra_last_error().decode()
+    a.workspace, a.workspace_bytes = (1 << 20) * 20, 1024 * 16 * 4 - 4
+    assert lib.fra_bwd_varlen(a, None) == _lib.FRA_EINVAL

@@ -1,0 +1,180 @@
+"""Parity of the log-sum-exp output and the backward (libfra.so through
+``fused_rope_attention_fwd`` / ``fused_rope_attention_bwd`` and autograd)
+with the CPU oracle on the same seeded inputs.
+
+The reference is forward-only, so the oracle's gradients (pinned against
+torch autograd in float64 and finite differences in ``test_oracle.py``)
+are the target.  Tolerances, all against the fp32 oracle:
+
+* lse (natural log, values ~5-8): max-abs <= 1e-2, mean-abs <= 1e-3.  The
+  bf16 rounding of q_rot / k_rot alone moves it by up to 1.6e-3 (mean 4e-4)
+  in the rounding-point model (oracle mode "bf16").
+* dq, dk, dv in bf16 (magnitudes <= ~1.5): max-abs <= 2e-2 and mean-abs <=
+  2e-3 (the forward's north-star bounds), and mean-abs <= 1e-2 x mean |ref|.
+  The rounding-point model of the kernels (q_rot/k_rot, P, dZ and the
+  results rounded to bf16) sits at 3-4e-3 x mean |ref| and <= 1e-2 x max |ref|.
+
+At full sizes, size-independent identities of the gradient cover what the
+oracle cannot: per (segment, head), sum over keys of dv = sum over queries of
+dout (rows of P sum to 1), and with cos = 1, sin = 0, sum over keys of dk = 0
+(rows of dZ sum to 0).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from fused_rope_attn_amd import fused_rope_attention, fused_rope_attention_bwd, fused_rope_attention_fwd
+from oracle import attention as A
+
+pytestmark = pytest.mark.gpu
+
+LSE_MAX, LSE_MEAN = 1e-2, 1e-3
+G_MAX, G_MEAN, G_REL_MEAN = 2e-2, 2e-3, 1e-2
+
+
+def f32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def make_case(lens, h, d, seed, dtype=torch.bfloat16, width=None, lead_rows=0, extra_rows=0):
+    """Segments of the given lengths (0 allowed) starting at row lead_rows,
+    with extra_rows rows after the last segment; random angles per token."""
+    cu = (lead_rows + np.concatenate([[0], np.cumsum(lens)])).astype(np.int32)
+    n = int(cu[-1]) + extra_rows
+    g = torch.Generator().manual_seed(seed)
+    q, k, v, do = (torch.randn(n, h, d, generator=g) for _ in range(4))
+    w = d // 2 if width is None else width
+    ang = torch.rand(n, w, generator=g) * 2 * math.pi - math.pi
+    return {"q": q.to(dtype), "k": k.to(dtype), "v": v.to(dtype), "dout": do.to(dtype),
+            "cos": ang.cos(), "sin": ang.sin(), "cu": torch.from_numpy(cu), "max_seqlen": int(max(lens))}
+
+
+def on(case, device):
+    return {k: (v.to(device) if torch.is_tensor(v) else v) for k, v in case.items()}
+
+
+def gpu_fwd_bwd(c):
+    out, lse = fused_rope_attention_fwd(c["q"], c["k"], c["v"], c["cos"], c["sin"], c["cu"], c["max_seqlen"])
+    dq, dk, dv = fused_rope_attention_bwd(c["dout"], c["q"], c["k"], c["v"], c["cos"], c["sin"], out, lse, c["cu"],
+                                          c["max_seqlen"])
+    torch.cuda.synchronize()
+    return out, lse, dq, dk, dv
+
+
+def check_grad(got, ref, what):
+    covered = ~np.isnan(ref)
+    assert covered.any()
+    err = np.abs(got[covered] - ref[covered])
+    assert np.isfinite(got[covered]).all(), f"{what}: non-finite gradient"
+    mx, mn, rm = float(err.max()), float(err.mean()), float(np.abs(ref[covered]).mean())
+    assert mx <= G_MAX and mn <= G_MEAN and mn <= G_REL_MEAN * rm, (
+        f"{what}: max-abs {mx:.3e} (<= {G_MAX}), mean-abs {mn:.3e} (<= {G_MEAN} and <= {G_REL_MEAN} x {rm:.3e})")
+    # rows outside every segment: zero (freshly allocated results)
+    assert np.all(got[~covered] == 0), f"{what}: rows outside the segments were written"
+
+
+def check_lse(got, ref, what):
+    covered = ~np.isnan(ref)
+    err = np.abs(got[covered] - ref[covered])
+    assert np.isfinite(got[covered]).all(), f"{what}: non-finite lse"
+    mx, mn = float(err.max()), float(err.mean())
+    assert mx <= LSE_MAX and mn <= LSE_MEAN, f"{what}: lse max-abs {mx:.3e} (<= {LSE_MAX}), mean {mn:.3e}"
+
+
+CASES = [
+    # (lens, heads, head_dim, width, dtype, lead_rows, extra_rows)
+    ([64, 64, 40, 1], 2, 80, None, torch.bfloat16, 0, 0),      # window kernels (2 waves)
+    ([64, 0, 17, 64], 3, 72, None, torch.bfloat16, 2, 3),      # window, empty segment, uncovered rows
+    ([33, 64], 2, 64, 64, torch.float16, 0, 1),               # window, full-width tables, fp16
+    ([300, 130], 2, 72, None, torch.bfloat16, 0, 0),          # long kernels (4 waves)
+    ([65, 0, 257], 2, 80, None, torch.bfloat16, 5, 2),        # long, empty segment, uncovered rows
+    ([200], 1, 96, 96, torch.bfloat16, 0, 0),                 # long, full-width tables
+    ([150, 70], 2, 128, None, torch.float16, 0, 0),           # long, head_dim 128, fp16
+    ([1000], 1, 80, None, torch.bfloat16, 0, 0),              # long, many key/query blocks
+]
+
+
+@pytest.mark.parametrize("ci", range(len(CASES)))
+def test_lse_and_backward_match_oracle(device, ci):
+    lens, h, d, width, dtype, lead, extra = CASES[ci]
+    case = make_case(lens, h, d, seed=500 + ci, dtype=dtype, width=width, lead_rows=lead, extra_rows=extra)
+    print(f"case {ci}: lens={lens} h={h} d={d} width={width} dtype={dtype}", flush=True)
+    out, lse, dq, dk, dv = gpu_fwd_bwd(on(case, device))
+    q, k, v, do = (f32(case[x]) for x in ("q", "k", "v", "dout"))
+    cos, sin, cu = f32(case["cos"]), f32(case["sin"]), case["cu"].numpy()
+    ref_lse = A.softmax_lse(q, k, cos, sin, cu)
+    check_lse(f32(lse), ref_lse, f"case {ci}")
+    rq, rk, rv = A.fused_rope_attention_bwd(do, q, k, v, cos, sin, cu)
+    what = f"case {ci} lens={lens} d={d}"
+    check_grad(f32(dq), rq, what + " dq")
+    check_grad(f32(dk), rk, what + " dk")
+    check_grad(f32(dv), rv, what + " dv")
+
+
+@pytest.mark.parametrize("lens,d", [([64, 64, 64], 80), ([513], 72)])
+def test_autograd_matches_functional(device, lens, d):
+    case = on(make_case(lens, 2, d, seed=600), device)
+    q, k, v = (case[x].clone().requires_grad_(True) for x in ("q", "k", "v"))
+    out = fused_rope_attention(q, k, v, case["cos"], case["sin"], case["cu"], case["max_seqlen"])
+    out.backward(case["dout"])
+    _, _, dq, dk, dv = gpu_fwd_bwd(case)
+    out_ng = fused_rope_attention(case["q"], case["k"], case["v"], case["cos"], case["sin"], case["cu"],
+                                  case["max_seqlen"])
+    torch.cuda.synchronize()
+    assert torch.equal(out.detach(), out_ng)
+    assert torch.equal(q.grad, dq) and torch.equal(k.grad, dk) and torch.equal(v.grad, dv)
+
+
+def test_forward_lse_does_not_change_output(device):
+    # the lse write is an extra store; the output is bit-identical with or without it
+    for lens, d in (([64, 40], 80), ([700], 80)):
+        c = on(make_case(lens, 2, d, seed=610), device)
+        out, _ = fused_rope_attention_fwd(c["q"], c["k"], c["v"], c["cos"], c["sin"], c["cu"], c["max_seqlen"])
+        ref = fused_rope_attention(c["q"], c["k"], c["v"], c["cos"], c["sin"], c["cu"], c["max_seqlen"])
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+
+
+def test_backward_deterministic(device):
+    c = on(make_case([1000, 64], 2, 80, seed=620), device)
+    a = gpu_fwd_bwd(c)
+    b = gpu_fwd_bwd(c)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def _segment_sums(x, cu):
+    """[nseg, H, D] float64 sums of x's rows over each segment."""
+    x = x.double()
+    cs = torch.cat([torch.zeros_like(x[:1]), x.cumsum(0)])
+    cu = cu.long()
+    return cs[cu[1:]] - cs[cu[:-1]]
+
+
+@pytest.mark.parametrize("nseg,L,h", [(144, 64, 16), (1, 9216, 2)])
+def test_backward_identities_full_size(device, nseg, L, h):
+    """BASELINE sizes (cfg2 window layer; cfg2 full layer at 2 of 16 heads):
+    sum_keys dv = sum_queries dout per (segment, head); with the identity
+    rotation, sum_keys dk = 0 per (segment, head)."""
+    d = 80
+    n = nseg * L
+    g = torch.Generator(device=device).manual_seed(630)
+    q, k, v, do = (torch.randn(n, h, d, generator=g, device=device).to(torch.bfloat16) for _ in range(4))
+    cu = torch.arange(0, n + 1, L, dtype=torch.int32, device=device)
+    cos = torch.ones(n, d // 2, device=device)
+    sin = torch.zeros(n, d // 2, device=device)
+    out, lse = fused_rope_attention_fwd(q, k, v, cos, sin, cu, L)
+    dq, dk, dv = fused_rope_attention_bwd(do, q, k, v, cos, sin, out, lse, cu, L)
+    torch.cuda.synchronize()
+    for t in (lse, dq, dk, dv):
+        assert torch.isfinite(t).all()
+    sdv, sdo = _segment_sums(dv, cu), _segment_sums(do, cu)
+    # dv rows are bf16-rounded sums of L products: compare at the scale of a row sum
+    tol = 2e-2 * float(sdo.abs().mean()) + 1e-2
+    assert float((sdv - sdo).abs().max()) <= tol * 4, float((sdv - sdo).abs().max())
+    assert float((sdv - sdo).abs().mean()) <= tol, float((sdv - sdo).abs().mean())
+    sdk = _segment_sums(dk, cu)
+    dk_row = float(dk.double().abs().mean())
+    assert float(sdk.abs().mean()) <= 0.05 * dk_row * math.sqrt(L), (float(sdk.abs().mean()), dk_row)

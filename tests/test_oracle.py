@@ -163,3 +163,119 @@ def test_round_bf16_matches_torch():
     np.testing.assert_array_equal(NUM.round_bf16(x), ref)
     np.testing.assert_array_equal(NUM.from_bf16_bits(NUM.bf16_bits(x)), ref)
     assert np.isnan(NUM.round_bf16(np.array([np.nan], np.float32)))[0]
+
+
+# ---- softmax statistics and gradients (the build's backward) ------------------
+
+
+def _torch_f64_forward(q, k, v, c, s, cu, scale=None):
+    """The unfused path in float64 torch ops (rotate_half form, per-segment
+    softmax attention), differentiable by autograd: an implementation that
+    shares no code with the oracle's backward."""
+    d = q.shape[-1]
+    half = d // 2
+    c, s = torch.from_numpy(c).double(), torch.from_numpy(s).double()
+    if c.shape[-1] == half:
+        c, s = torch.cat([c, c], -1), torch.cat([s, s], -1)
+    c, s = c[:, None, :], s[:, None, :]
+
+    def rot(x):
+        rh = torch.cat([-x[..., half:], x[..., :half]], -1)
+        return x * c + rh * s
+
+    qr, kr = rot(q), rot(k)
+    scale = d ** -0.5 if scale is None else scale
+    outs = []
+    for a, b in A.segments(cu, q.shape[0]):
+        p = torch.softmax(torch.einsum("ihd,jhd->hij", qr[a:b], kr[a:b]) * scale, -1)
+        outs.append((a, b, torch.einsum("hij,jhd->ihd", p, v[a:b])))
+    out = torch.zeros_like(q)
+    for a, b, o in outs:
+        out = out.index_copy(0, torch.arange(a, b), o)
+    return out
+
+
+@pytest.mark.parametrize("d,width,cu", [
+    (8, 4, [0, 7, 7, 25, 40]),   # half-width tables, an empty segment
+    (8, 8, [0, 13, 40]),         # full-width tables (second half rotates by its own angles)
+    (12, 6, [3, 4, 30]),         # L=1 segment, rows outside every segment
+])
+def test_oracle_backward_vs_torch_autograd(d, width, cu):
+    n, h = 40, 2
+    q, k, v, g = (rand((n, h, d), 20 + i) for i in range(4))
+    c, s = rand_tables(n, d // 2, 24, width)
+    dq, dk, dv = A.fused_rope_attention_bwd(g, q, k, v, c, s, cu, softmax_scale=0.6)
+    tq, tk, tv = (torch.from_numpy(x).double().requires_grad_(True) for x in (q, k, v))
+    _torch_f64_forward(tq, tk, tv, c, s, cu, scale=0.6).backward(torch.from_numpy(g).double())
+    covered = ~np.isnan(dq)
+    rows = np.zeros(n, bool)
+    for a, b in A.segments(cu, n):
+        rows[a:b] = True
+    assert np.array_equal(covered.all(axis=(1, 2)), rows)
+    for got, ref in ((dq, tq.grad), (dk, tk.grad), (dv, tv.grad)):
+        np.testing.assert_allclose(got[covered], ref.numpy()[covered], rtol=1e-4, atol=2e-6)
+
+
+def test_oracle_backward_finite_differences_vs_brute_force():
+    """Directional derivative of L = sum(dout * O) along random directions,
+    O from the element-by-element float64 brute force, against the oracle's
+    gradient."""
+    n, h, d = 9, 1, 8
+    cu = [0, 4, 9]
+    q, k, v, g = (rand((n, h, d), 40 + i).astype(np.float64) for i in range(4))
+    c, s = rand_tables(n, d // 2, 44, d)
+    dq, dk, dv = A.fused_rope_attention_bwd(g, q, k, v, c, s, cu)
+    eps = 1e-5
+    for which, grad in ((0, dq), (1, dk), (2, dv)):
+        direction = np.random.default_rng(50 + which).standard_normal((n, h, d))
+
+        def loss(t):
+            args = [q, k, v]
+            args[which] = args[which] + t * direction
+            return float((A.brute_force_f64(*args, c, s, cu) * g).sum())
+
+        fd = (loss(eps) - loss(-eps)) / (2 * eps)
+        assert abs(fd - float((grad * direction).sum())) <= 1e-4 * max(1.0, abs(fd)), (which, fd)
+
+
+def test_softmax_lse_vs_scipy_logsumexp():
+    from scipy.special import logsumexp
+    n, h, d = 30, 2, 8
+    cu = [0, 11, 11, 30]
+    q, k = rand((n, h, d), 60), rand((n, h, d), 61)
+    c, s = rand_tables(n, d // 2, 62)
+    got = A.softmax_lse(q, k, c, s, cu, softmax_scale=0.8)
+    qr, kr = A.rotate(q, c, s).astype(np.float64), A.rotate(k, c, s).astype(np.float64)
+    for a, b in A.segments(cu, n):
+        for hh in range(h):
+            ref = logsumexp(qr[a:b, hh] @ kr[a:b, hh].T * 0.8, axis=1)
+            np.testing.assert_allclose(got[hh, a:b], ref, rtol=1e-6, atol=1e-6)
+
+
+def test_backward_identities():
+    """Rows of P sum to 1, so per segment the sum over keys of dv equals the
+    sum over queries of dout; rows of dZ sum to 0, so with the identity
+    rotation the sum over keys of dk is 0; a one-token segment has dq = dk = 0
+    and dv = dout."""
+    n, h, d = 50, 2, 8
+    cu = [0, 1, 20, 50]
+    q, k, v, g = (rand((n, h, d), 70 + i) for i in range(4))
+    c, s = np.ones((n, d // 2), np.float32), np.zeros((n, d // 2), np.float32)
+    dq, dk, dv = A.fused_rope_attention_bwd(g, q, k, v, c, s, cu)
+    for a, b in zip(cu[:-1], cu[1:]):
+        np.testing.assert_allclose(dv[a:b].sum(0), g[a:b].sum(0), rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(dk[a:b].sum(0), 0.0, atol=1e-5)
+    np.testing.assert_allclose(dq[0], 0.0, atol=1e-7)
+    np.testing.assert_allclose(dv[0], g[0], atol=1e-7)
+
+
+def test_backward_emulation_close_to_fp32():
+    n, h, d = 128, 2, 16
+    cu = [0, 64, 128]
+    q, k, v, g = (NUM.round_bf16(rand((n, h, d), 80 + i)) for i in range(4))
+    c, s = rand_tables(n, d // 2, 84)
+    ref = A.fused_rope_attention_bwd(g, q, k, v, c, s, cu)
+    emu = A.fused_rope_attention_bwd(g, q, k, v, c, s, cu, mode="bf16")
+    for r, e in zip(ref, emu):
+        assert np.abs(r - e).mean() <= 1e-2 * np.abs(r).mean()
+        assert np.abs(r - e).max() <= 2e-2 * np.abs(r).max()
