@@ -36,8 +36,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
-from fused_rope_attn_amd import fused_rope_attention, plan  # noqa: E402
-from fused_rope_attn_amd.configs import WORKLOADS, algorithmic_bytes, algorithmic_flops, make_inputs  # noqa: E402
+from fused_rope_attn_amd import (fused_rope_attention, fused_rope_attention_bwd,  # noqa: E402
+                                 fused_rope_attention_fwd, plan)
+from fused_rope_attn_amd.configs import (WORKLOADS, algorithmic_bytes, algorithmic_bytes_bwd,  # noqa: E402
+                                         algorithmic_flops, algorithmic_flops_bwd, make_inputs)
 
 METRIC = "µs/call fused RoPE+varlen attn (1344² window layer); % HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
@@ -90,6 +92,29 @@ def measure(inp, steps: int, warmup: int, flush: torch.Tensor) -> dict:
     def call():
         fused_rope_attention(q, k, v, cos, sin, cu, ms, out=out)
 
+    return time_calls(call, steps, warmup, flush)
+
+
+def backward_call(inp):
+    """A closure running one backward (``fused_rope_attention_bwd``: the
+    row-dot, dq and dk/dv kernels) on the workload, with dO ~ N(0, 1) and
+    the forward's out and lse computed once beforehand."""
+    q, k, v, cos, sin, cu = (inp[x] for x in ("q", "k", "v", "cos", "sin", "cu_seqlens"))
+    ms = inp["max_seqlen"]
+    out, lse = fused_rope_attention_fwd(q, k, v, cos, sin, cu, ms)
+    g = torch.Generator(device=q.device).manual_seed(99)
+    dout = torch.randn(q.shape, generator=g, device=q.device).to(q.dtype)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+
+    def call():
+        fused_rope_attention_bwd(dout, q, k, v, cos, sin, out, lse, cu, ms, dq=dq, dk=dk, dv=dv)
+
+    return call
+
+
+def time_calls(call, steps: int, warmup: int, flush: torch.Tensor) -> dict:
+    """Cold (1 GiB read before each call) and warm (back-to-back) timings of
+    ``call`` with HIP events on torch's current stream, where the kernels run."""
     for _ in range(warmup):
         call()
     torch.cuda.synchronize()
@@ -177,6 +202,27 @@ def run_workload(name: str, steps: int, warmup: int, flush: torch.Tensor, dev) -
             "warm_achieved": (nbytes if hbm else flops) / (m["warm_us"] * 1e-6) / (1e9 if hbm else 1e12)}, inp
 
 
+def run_backward(name: str, steps: int, warmup: int, flush: torch.Tensor, dev) -> dict:
+    w = WORKLOADS[name]
+    inp = make_inputs(w, seed=1234 + list(WORKLOADS).index(name), device=dev)
+    cu = inp["cu_seqlens"].cpu()
+    lens = (cu[1:] - cu[:-1]).tolist()
+    n = int(cu[-1])
+    cos = inp["cos"]
+    nbytes = algorithmic_bytes_bwd(n, w.heads, w.head_dim, inp["q"].element_size(), cos.shape[1],
+                                   cos.element_size(), len(lens))
+    flops = algorithmic_flops_bwd(w.heads, w.head_dim, lens)
+    m = time_calls(backward_call(inp), steps, warmup, flush)
+    t = m["cold_median_us"] * 1e-6
+    hbm = w.kind == "window"
+    achieved = nbytes / t / 1e9 if hbm else flops / t / 1e12
+    peak = HBM_PEAK_GBS if hbm else MFMA_BF16_PEAK_TFLOPS
+    return {"workload": name, "direction": "backward", "note": w.note, "tokens": n, "segments": len(lens),
+            "max_seqlen": max(lens), "heads": w.heads, "head_dim": w.head_dim, "bytes": nbytes, "flops": flops, **m,
+            "roofline": {"bound": "hbm" if hbm else "mfma", "achieved": achieved, "peak": peak,
+                         "unit": "GB/s" if hbm else "TFLOP/s", "frac": achieved / peak}}
+
+
 def profile_driver(args, flush, dev) -> int:
     """Kernel launches for rocprofv3: warmup, then ``--profile-calls`` calls of
     the workload each after a cache flush, then one copy of known size whose
@@ -186,11 +232,16 @@ def profile_driver(args, flush, dev) -> int:
     inp = make_inputs(w, seed=1234 + list(WORKLOADS).index(args.workload), device=dev)
     q, k, v, cos, sin, cu = (inp[x] for x in ("q", "k", "v", "cos", "sin", "cu_seqlens"))
     out = torch.empty_like(q)
+    if args.bwd:
+        call = backward_call(inp)
+    else:
+        def call():
+            fused_rope_attention(q, k, v, cos, sin, cu, inp["max_seqlen"], out=out)
     for _ in range(3):
-        fused_rope_attention(q, k, v, cos, sin, cu, inp["max_seqlen"], out=out)
+        call()
     for i in range(args.profile_calls):
         evict(flush)
-        fused_rope_attention(q, k, v, cos, sin, cu, inp["max_seqlen"], out=out)
+        call()
     torch.cuda.synchronize()
     n = args.copy_mib << 20
     src = torch.ones(n // 4, dtype=torch.float32, device=dev)
@@ -200,7 +251,12 @@ def profile_driver(args, flush, dev) -> int:
     torch.cuda.synchronize()
     n_tok, lens, nbytes, flops = workload_cost(w, inp)
     pl = plan(q, k, v, cos, sin, cu, max_seqlen=inp["max_seqlen"])
-    print(json.dumps({"profile_driver": args.workload, "kernel": pl["name"], "warmup_calls": 3,
+    if args.bwd:
+        nbytes = algorithmic_bytes_bwd(n_tok, w.heads, w.head_dim, q.element_size(), cos.shape[1],
+                                       cos.element_size(), len(lens))
+        flops = algorithmic_flops_bwd(w.heads, w.head_dim, lens)
+    print(json.dumps({"profile_driver": args.workload, "direction": "backward" if args.bwd else "forward",
+                      "kernel": pl["name"], "warmup_calls": 3,
                       "calls": args.profile_calls, "bytes": nbytes, "flops": flops,
                       "copy_bytes_each_way": n}), flush=True)
     return 0
@@ -289,6 +345,9 @@ def main() -> int:
                     help="profiling driver: run this many cold calls of --workload, then a plain "
                          "device copy of --copy-mib MiB (HBM counter calibration), and exit")
     ap.add_argument("--copy-mib", type=int, default=256)
+    ap.add_argument("--bwd", action="store_true", help="profiling driver: run backward calls instead")
+    ap.add_argument("--backward", default=None, metavar="FILE",
+                    help="measure the backward of every workload and write them to FILE")
     ap.add_argument("--drift", default=None, metavar="FILE",
                     help="run the 32-layer drift stack on --workload's grid and write the report to FILE")
     args = ap.parse_args()
@@ -304,6 +363,16 @@ def main() -> int:
     flush = torch.ones(FLUSH_BYTES, dtype=torch.uint8, device=dev)
     if args.profile_calls:
         return profile_driver(args, flush, dev)
+    if args.backward:
+        rows = []
+        for name in WORKLOADS:
+            r = run_backward(name, max(10, args.steps // 2), max(3, args.warmup // 2), flush, dev)
+            rows.append(r)
+            print(f"[bench] backward {name}: cold {r['cold_median_us']:.1f} us, warm {r['warm_us']:.1f} us, "
+                  f"{r['roofline']['frac'] * 100:.1f}% of {r['roofline']['bound']}", file=sys.stderr, flush=True)
+        with open(args.backward, "w") as f:
+            json.dump(rows, f, indent=1)
+        return 0
     if args.drift:
         rep = drift_stack(args.workload, dev)
         with open(args.drift, "w") as f:

@@ -26,7 +26,8 @@ import torch
 from .fused_attn import compute_rope_2d
 from .utils import get_window_index
 
-__all__ = ["Workload", "WORKLOADS", "make_inputs", "algorithmic_bytes", "algorithmic_flops"]
+__all__ = ["Workload", "WORKLOADS", "make_inputs", "algorithmic_bytes", "algorithmic_flops",
+           "algorithmic_bytes_bwd", "algorithmic_flops_bwd"]
 
 
 @dataclass(frozen=True)
@@ -107,3 +108,19 @@ def algorithmic_bytes(n: int, heads: int, head_dim: int, elem_bytes: int, rope_w
 def algorithmic_flops(heads: int, head_dim: int, seg_lens) -> int:
     """QK^T plus PV flops at the real head_dim, non-causal: 4*D*H*sum(L^2)."""
     return int(4 * head_dim * heads * sum(int(x) * int(x) for x in seg_lens))
+
+
+def algorithmic_bytes_bwd(n: int, heads: int, head_dim: int, elem_bytes: int, rope_width: int,
+                          rope_bytes: int, nseg: int) -> int:
+    """HBM bytes one backward call must move at least: read Q, K, V, O and
+    dO and write dQ, dK, dV once each, read cos and sin, the forward's
+    log-sum-exp ([H, N] fp32) and cu_seqlens."""
+    return (8 * n * heads * head_dim * elem_bytes + 2 * n * rope_width * rope_bytes + 4 * n * heads
+            + 4 * (nseg + 1))
+
+
+def algorithmic_flops_bwd(heads: int, head_dim: int, seg_lens) -> int:
+    """The backward's five products per (segment, head) at the real head_dim
+    -- S = QK^T (recomputed), dP = dO V^T, dV = P^T dO, dQ = dS K,
+    dK = dS^T Q -- 2*L*L*D flops each: 10*D*H*sum(L^2)."""
+    return int(10 * head_dim * heads * sum(int(x) * int(x) for x in seg_lens))

@@ -59,10 +59,10 @@ struct KParams {
 
 // ---- window kernel ------------------------------------------------------------
 //
-// One workgroup of HW wavefronts per (segment, group of HW heads), HW = 4,
-// or 2 when a layer has too few windows to fill the chip; segment length
-// L <= 64.  All HBM traffic is coalesced: consecutive lanes move
-// consecutive 16-byte chunks of the group's slab -- 4 heads x D elements,
+// One workgroup of HW wavefronts per (segment, group of HW heads), HW = 2
+// when that grid fits in one round of resident workgroups, else 4; segment
+// length L <= 64.  All HBM traffic is coalesced: consecutive lanes move
+// consecutive 16-byte chunks of the group's slab -- HW heads x D elements,
 // contiguous in a [tokens, heads, head_dim] tensor -- and LDS turns the slab
 // into MFMA operands (and the output back into slab rows).
 //
@@ -70,7 +70,7 @@ struct KParams {
 //      front;
 //   2. per 32-token half: the half's cos/sin rows -> LDS as fp32 rows, the
 //      half's Q slab rows -> LDS, where wavefront w rotates the quads of head
-//      4*hg + w it feeds (fp32, rounded to the storage dtype); then the same
+//      HW*hg + w it feeds (fp32, rounded to the storage dtype); then the same
 //      for K;
 //   3. the V slab goes from HBM straight to LDS (global_load_lds_dwordx4) as
 //      padded rows, over the dead staging buffers;
@@ -81,8 +81,9 @@ struct KParams {
 //
 // Nothing but the staging buffers of one half lives in LDS while Q and K are
 // rotated, and V never passes through registers, so at D = 80 a workgroup
-// needs 45 KB of LDS and three fit on a CU: a 144-window, 16-head layer (576
-// workgroups) runs in one round on 256 CUs.
+// needs 28 KB of LDS with two heads (five fit on a CU) or 44 KB with four
+// (three fit): a 144-window, 16-head layer (1152 two-head workgroups) runs in
+// one round on 256 CUs.
 //
 // Rows past the segment (L < 64) load the segment's first (Q, K) or last (V)
 // row: finite values whose keys are masked and whose queries are not stored.
