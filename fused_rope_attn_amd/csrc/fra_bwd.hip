@@ -16,8 +16,10 @@
 // q_rot / k_rot is taken as the identity, as autograd does for a cast).  P is
 // recomputed from the forward's log-sum-exp: P = exp2(z log2(e) - lse log2(e)).
 //
-// Both matrix kernels use v_mfma_f32_32x32x16_{bf16,f16} with the operand
-// layouts of the forward (fra_kernels.hip):
+// Segments of at most 64 tokens take one kernel, bwd_window_kernel, that does
+// all of it per (segment, head) in one pass (below).  Longer segments take
+// three: bwd_dot_kernel, then two matrix kernels with the operand layouts of
+// the forward (fra_kernels.hip), v_mfma_f32_32x32x16_{bf16,f16}:
 //   bwd_dq_kernel    one workgroup per block of 32*NW queries; lane (r, g) of
 //                    wave w holds query 32w + r as the column of S^T, dP^T and
 //                    dQ^T (the forward's layout), looping over 64-key blocks of
@@ -86,49 +88,116 @@ template <int D> struct BwdOcc {
 constexpr int kBwdBlockQ = 64;   // queries per LDS stage of the dk/dv kernel
 constexpr int kBwdBlockKV = 64;  // keys per LDS stage of the dq kernel
 
-// Rows [0, nrows) of a block whose row 0 is token tok0 of x: the split-half
-// rotation (fp32, rounded to the storage dtype, as the forward computes it)
-// into LDS rows [x0r | x1r | 0-pad to a multiple of 16].  Rows >= nvalid are
-// zero.  x points at token tok0's row of the head; xs is its row stride in
-// bytes.
-template <int D, class E, bool FULL>
-__device__ __forceinline__ void stage_rotated(char *dst, int pitch, const BParams &p, const char *x, int64_t xs,
-                                              int tok0, int nvalid, int nrows, int tid, int nthr) {
-    constexpr int NQ = D / 8;  // quads per half
-    constexpr int HALF = D / 2;
-    constexpr int PADQ = (bwd_dp(D) - D) / 4;
-    constexpr int PER = NQ + PADQ;
-    for (int it = tid; it < nrows * PER; it += nthr) {
-        const int row = it / PER, i = it - row * PER;
-        char *drow = dst + row * pitch;
-        if (i >= NQ) {
-            *(u32x2 *)(drow + 2 * D + 8 * (i - NQ)) = u32x2{0u, 0u};
-            continue;
-        }
-        const bool valid = row < nvalid;
-        const int rr = valid ? row : 0;
-        const int64_t tok = (int64_t)tok0 + rr;
-        u32x2 r0, r1;
-        load_rotate_quad<D, E, FRA_DTYPE_F32, FULL>(x + rr * xs, p.cos + tok * p.sr_s * 4, p.sin + tok * p.sr_s * 4,
-                                                    i, valid, r0, r1);
-        *(u32x2 *)(drow + 8 * i) = r0;
-        *(u32x2 *)(drow + 2 * HALF + 8 * i) = r1;
-    }
-}
+// A block of NROWS rows staged through registers: every global load of the
+// block is issued first (the item loops have compile-time trip counts and
+// unroll), then the values are rotated and written to LDS, so a block costs
+// one HBM round trip rather than one per item.
+//
+// RotBlock: the split-half rotation (fp32, rounded to the storage dtype, as
+// the forward computes it) of NX tensors that share token rows (and so their
+// cos/sin rows: q and k of one segment), into LDS rows [x0r | x1r | 0-pad to a
+// multiple of 16].  Item (row, i) is quad i (entries 4i..4i+3) of both halves.
+// Rows >= nvalid are zero.  x[n] points at token tok0's row of the head; xs[n]
+// is its row stride in bytes.
+template <int D, class E, bool FULL, int NROWS, int NT, int NX>
+struct RotBlock {
+    static constexpr int NQ = D / 8, HALF = D / 2;
+    static constexpr int N = NROWS * NQ, K = (N + NT - 1) / NT;
+    static constexpr int PADQ = (bwd_dp(D) - D) / 4;  // zero quads after each row
+    u32x2 x0[NX][K], x1[NX][K];
+    f32x4 c0[K], s0[K], c1[K], s1[K];
 
-// Rows [0, nrows) of x (row stride xs bytes) into LDS as 16-byte chunks,
-// zero past nvalid rows and past head_dim up to a multiple of 16.
-template <int D>
-__device__ __forceinline__ void stage_rows(char *dst, int pitch, const char *x, int64_t xs, int nvalid, int nrows,
-                                           int tid, int nthr) {
-    constexpr int CH = bwd_dp(D) / 8;
-    for (int it = tid; it < nrows * CH; it += nthr) {
-        const int row = it / CH, c = it - row * CH;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (row < nvalid && c < D / 8) v = *(const u32x4 *)(x + row * xs + 16 * c);
-        *(u32x4 *)(dst + row * pitch + 16 * c) = v;
+    __device__ __forceinline__ void load(const BParams &p, const char *const (&x)[NX], const int64_t (&xs)[NX],
+                                         int tok0, int nvalid, int tid) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int it = tid + k * NT;
+            if (N % NT == 0 || it < N) {
+                const int row = it / NQ, i = it - row * NQ;
+                const int rr = row < nvalid ? row : 0;
+                const int64_t tok = (int64_t)tok0 + rr;
+#pragma unroll
+                for (int n = 0; n < NX; ++n) {
+                    const char *xrow = x[n] + rr * xs[n];
+                    x0[n][k] = *(const u32x2 *)(xrow + 8 * i);
+                    x1[n][k] = *(const u32x2 *)(xrow + 2 * HALF + 8 * i);
+                }
+                const char *crow = p.cos + tok * p.sr_s * 4, *srow = p.sin + tok * p.sr_s * 4;
+                c0[k] = *(const f32x4 *)(crow + 16 * i);
+                s0[k] = *(const f32x4 *)(srow + 16 * i);
+                if constexpr (FULL) {
+                    c1[k] = *(const f32x4 *)(crow + 4 * (HALF + 4 * i));
+                    s1[k] = *(const f32x4 *)(srow + 4 * (HALF + 4 * i));
+                }
+            }
+        }
     }
-}
+
+    __device__ __forceinline__ void store(char *const (&dst)[NX], int pitch, int nvalid, int tid) const {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int it = tid + k * NT;
+            if (N % NT == 0 || it < N) {
+                const int row = it / NQ, i = it - row * NQ;
+                const bool valid = row < nvalid;
+#pragma unroll
+                for (int n = 0; n < NX; ++n) {
+                    u32x2 r0, r1;
+                    rotate_quad<E>(valid ? x0[n][k] : u32x2{0u, 0u}, valid ? x1[n][k] : u32x2{0u, 0u}, c0[k], s0[k],
+                                   FULL ? c1[k] : c0[k], FULL ? s1[k] : s0[k], r0, r1);
+                    char *drow = dst[n] + row * pitch;
+                    *(u32x2 *)(drow + 8 * i) = r0;
+                    *(u32x2 *)(drow + 2 * HALF + 8 * i) = r1;
+                }
+            }
+        }
+        if constexpr (PADQ > 0) {
+            for (int it = tid; it < NROWS * PADQ; it += NT) {
+                const int row = it / PADQ, i = it - row * PADQ;
+#pragma unroll
+                for (int n = 0; n < NX; ++n) *(u32x2 *)(dst[n] + row * pitch + 2 * D + 8 * i) = u32x2{0u, 0u};
+            }
+        }
+    }
+};
+
+// RowBlock: rows of x copied as 16-byte chunks, zero past nvalid rows and
+// past head_dim up to a multiple of 16.
+template <int D, int NROWS, int NT>
+struct RowBlock {
+    static constexpr int CH = D / 8, N = NROWS * CH, K = (N + NT - 1) / NT;
+    static constexpr int PADC = bwd_dp(D) / 8 - CH;  // zero chunks after each row
+    u32x4 v[K];
+
+    __device__ __forceinline__ void load(const char *x, int64_t xs, int nvalid, int tid) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int it = tid + k * NT;
+            v[k] = u32x4{0u, 0u, 0u, 0u};
+            if (N % NT == 0 || it < N) {
+                const int row = it / CH, c = it - row * CH;
+                if (row < nvalid) v[k] = *(const u32x4 *)(x + row * xs + 16 * c);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(char *dst, int pitch, int tid) const {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int it = tid + k * NT;
+            if (N % NT == 0 || it < N) {
+                const int row = it / CH, c = it - row * CH;
+                *(u32x4 *)(dst + row * pitch + 16 * c) = v[k];
+            }
+        }
+        if constexpr (PADC > 0) {
+            for (int it = tid; it < NROWS * PADC; it += NT) {
+                const int row = it / PADC, c = CH + (it - row * PADC);
+                *(u32x4 *)(dst + row * pitch + 16 * c) = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    }
+};
 
 // fp32 gradient rows of x_rot (LDS, `fpf` floats per row) -> gradient of x:
 // the transpose of the forward's rotation, x0r = x0 c0 - x1 s0,
@@ -246,8 +315,14 @@ void bwd_dq_kernel(const BParams p) {
     const int nq = min(BQ, L - q0);
 
     // Q_rot of the block -> LDS -> the B operands of S^T (one query per lane).
-    stage_rotated<D, E, FULL>(lds, PRD, p, p.q + ((int64_t)(s0 + q0) * p.sq_s + (int64_t)head * p.sq_h) * 2,
-                              p.sq_s * 2, s0 + q0, nq, BQ, tid, NT);
+    {
+        RotBlock<D, E, FULL, BQ, NT, 1> qb;
+        const char *const xq[1] = {p.q + ((int64_t)(s0 + q0) * p.sq_s + (int64_t)head * p.sq_h) * 2};
+        const int64_t xs[1] = {p.sq_s * 2};
+        qb.load(p, xq, xs, s0 + q0, nq, tid);
+        char *const dst[1] = {lds};
+        qb.store(dst, PRD, nq, tid);
+    }
     __syncthreads();
     const int qi = 32 * w + r;
     const bool qvalid = qi < nq;
@@ -272,12 +347,21 @@ void bwd_dq_kernel(const BParams p) {
     const int nkb = (L + BKV - 1) / BKV;
     for (int kb = 0; kb < nkb; ++kb) {
         const int k0 = kb * BKV, nk = min(BKV, L - k0);
-        __syncthreads();  // the previous block's (or Q's) LDS reads are done
-        stage_rotated<D, E, FULL>(lds + kKr, PTR, p,
-                                  p.k + ((int64_t)(s0 + k0) * p.sk_s + (int64_t)head * p.sk_h) * 2, p.sk_s * 2,
-                                  s0 + k0, nk, BKV, tid, NT);
-        stage_rows<D>(lds + kV, PRD, p.v + ((int64_t)(s0 + k0) * p.sv_s + (int64_t)head * p.sv_h) * 2, p.sv_s * 2,
-                      nk, BKV, tid, NT);
+        {
+            RotBlock<D, E, FULL, BKV, NT, 1> kbk;
+            RowBlock<D, BKV, NT> vbk;
+            const char *const xk[1] = {p.k + ((int64_t)(s0 + k0) * p.sk_s + (int64_t)head * p.sk_h) * 2};
+            const int64_t xs[1] = {p.sk_s * 2};
+            // an opaque thread id: the items' addresses are recomputed per
+            // block instead of being kept live across the loop
+            const int ft = fresh(tid);
+            kbk.load(p, xk, xs, s0 + k0, nk, ft);
+            vbk.load(p.v + ((int64_t)(s0 + k0) * p.sv_s + (int64_t)head * p.sv_h) * 2, p.sv_s * 2, nk, ft);
+            __syncthreads();  // the previous block's (or Q's) LDS reads are done
+            char *const dst[1] = {lds + kKr};
+            kbk.store(dst, PTR, nk, ft);
+            vbk.store(lds + kV, PRD, ft);
+        }
         __syncthreads();
         // S^T = K_rot Q_rot^T and dP^T = V dout^T: rows key, column query.
         f32x16 sacc[2], dpacc[2];
@@ -361,8 +445,14 @@ void bwd_dkdv_kernel(const BParams p) {
     const int nk = min(BKV, L - k0);
 
     // K_rot and V of the block -> the B operands of S and dP (one key per lane).
-    stage_rotated<D, E, FULL>(lds, PRD, p, p.k + ((int64_t)(s0 + k0) * p.sk_s + (int64_t)head * p.sk_h) * 2,
-                              p.sk_s * 2, s0 + k0, nk, BKV, tid, NT);
+    {
+        RotBlock<D, E, FULL, BKV, NT, 1> kbk;
+        const char *const xk[1] = {p.k + ((int64_t)(s0 + k0) * p.sk_s + (int64_t)head * p.sk_h) * 2};
+        const int64_t xs[1] = {p.sk_s * 2};
+        kbk.load(p, xk, xs, s0 + k0, nk, tid);
+        char *const dst[1] = {lds};
+        kbk.store(dst, PRD, nk, tid);
+    }
     __syncthreads();
     const int ki = 32 * w + r;
     const bool kvalid = ki < nk;
@@ -388,17 +478,31 @@ void bwd_dkdv_kernel(const BParams p) {
     const int nqb = (L + BQ - 1) / BQ;
     for (int qb = 0; qb < nqb; ++qb) {
         const int q0 = qb * BQ, nq = min(BQ, L - q0);
-        __syncthreads();  // the previous block's (or K's) LDS reads are done
-        stage_rotated<D, E, FULL>(lds + kQr, PTR, p,
-                                  p.q + ((int64_t)(s0 + q0) * p.sq_s + (int64_t)head * p.sq_h) * 2, p.sq_s * 2,
-                                  s0 + q0, nq, BQ, tid, NT);
-        stage_rows<D>(lds + kDo, PTR, p.dout + ((int64_t)(s0 + q0) * p.sdo_s + (int64_t)head * p.sdo_h) * 2,
-                      p.sdo_s * 2, nq, BQ, tid, NT);
-        if (tid < BQ) {
+        {
+            RotBlock<D, E, FULL, BQ, NT, 1> qbk;
+            RowBlock<D, BQ, NT> dbk;
+            const char *const xq[1] = {p.q + ((int64_t)(s0 + q0) * p.sq_s + (int64_t)head * p.sq_h) * 2};
+            const int64_t xs[1] = {p.sq_s * 2};
+            // an opaque thread id: the items' addresses are recomputed per
+            // block instead of being kept live across the loop
+            const int ft = fresh(tid);
+            qbk.load(p, xq, xs, s0 + q0, nq, ft);
+            dbk.load(p.dout + ((int64_t)(s0 + q0) * p.sdo_s + (int64_t)head * p.sdo_h) * 2, p.sdo_s * 2, nq, ft);
             // Rows past the segment: lse = +inf makes their P (and dZ) zero.
-            const int64_t srow = (int64_t)head * p.total + s0 + q0 + tid;
-            ((float *)(lds + kLse))[tid] = tid < nq ? p.lse[srow] * kLog2e : __builtin_inff();
-            ((float *)(lds + kDv))[tid] = tid < nq ? p.dvec[srow] : 0.f;
+            float lv = __builtin_inff(), dvv = 0.f;
+            if (tid < nq) {
+                const int64_t srow = (int64_t)head * p.total + s0 + q0 + tid;
+                lv = p.lse[srow] * kLog2e;
+                dvv = p.dvec[srow];
+            }
+            __syncthreads();  // the previous block's (or K's) LDS reads are done
+            char *const dst[1] = {lds + kQr};
+            qbk.store(dst, PTR, nq, ft);
+            dbk.store(lds + kDo, PTR, ft);
+            if (tid < BQ) {
+                ((float *)(lds + kLse))[tid] = lv;
+                ((float *)(lds + kDv))[tid] = dvv;
+            }
         }
         __syncthreads();
 #pragma unroll
@@ -477,6 +581,248 @@ void bwd_dkdv_kernel(const BParams p) {
                                p.sdk_s * 2, s0 + k0, nk, tid, NT);
 }
 
+// ---- window layers: the whole backward of one (segment, head) in one pass -------------
+//
+// Segments of at most 64 tokens (every query block is every key block): one
+// workgroup of two wavefronts per (segment, head) stages Q_rot, K_rot, dO and
+// V once and produces dq, dk and dv, so each input is read from HBM once (the
+// two-kernel path reads q, k, v and dO twice and out and dO once more).
+//   phase 1  wave w owns queries 32w..32w+31 (the dq kernel's layout): Dvec of
+//            its queries from dO (LDS) and out (HBM), then S^T, dP^T, dZ^T and
+//            dQ^T = K_rot^T dZ^T; it takes its keys' K_rot and V rows as
+//            registers before the barrier that frees their LDS for dQ's rows;
+//   phase 2  wave w owns keys 32w..32w+31 (the dk/dv kernel's layout): S, dP,
+//            dZ, dV^T = dO^T P and dK^T = Q_rot^T dZ; dv is stored from
+//            registers and dk's rows go through LDS for the inverse rotation.
+template <int D> struct WinBwdLds {
+    static constexpr int PTR = bwd_pitch_tr(D), PRD = bwd_pitch_rows(D), FP = bwd_pitch_f32(D);
+    static constexpr int kKr = 0, kV = 64 * PTR, kQr = kV + 64 * PRD, kDo = kQr + 64 * PTR;
+    static constexpr int kLse = kDo + 64 * PTR, kDvec = kLse + 64 * 4;
+    static constexpr int kStage = kDvec + 64 * 4;
+    // fp32 rows of dQ over K_rot + V (dead once phase 1 holds its operands),
+    // then those of dK after it (over Q_rot and dO, dead after phase 2).
+    static constexpr int kFq = 0, kFk = 64 * FP;
+    static_assert(64 * FP <= kQr, "dQ rows must fit over the K_rot and V staging");
+    static constexpr int kBytes = cmax(kStage, 2 * 64 * FP);
+};
+
+template <int D, class E, bool FULL>
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(BwdOcc<D>::kWaves, BwdOcc<D>::kWaves)))
+void bwd_window_kernel(const BParams p) {
+    using LDS = WinBwdLds<D>;
+    constexpr int DP = bwd_dp(D), S = DP / 16, NDT = (D + 31) / 32;
+    constexpr int PTR = LDS::PTR, PRD = LDS::PRD, FP = LDS::FP;
+    constexpr int NT = 128;
+    __shared__ __attribute__((aligned(16))) char lds[LDS::kBytes];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 31, g = lane >> 5;
+    const int unit = xcd_remap(blockIdx.x, gridDim.x);
+    const int seg = unit / p.num_heads, head = unit - seg * p.num_heads;
+    int s0, L;
+    seg_bounds(p, seg, s0, L);
+    if (L <= 0) return;  // uniform
+    // Launched when max_seqlen <= 64; a longer segment (an understated
+    // max_seqlen) gets unspecified gradients, never an access past 64 rows.
+    L = min(L, 64);
+    const int64_t qoff = ((int64_t)s0 * p.sq_s + (int64_t)head * p.sq_h) * 2;
+    const int64_t koff = ((int64_t)s0 * p.sk_s + (int64_t)head * p.sk_h) * 2;
+    const int row = 32 * w + (lane & 31);  // phase 1: this lane's query; phase 2: its key
+    const bool rvalid = row < L;
+    // Every load of the workgroup first (one HBM round trip), then the
+    // rotations and LDS writes.  q and k share their cos/sin loads.
+    u32x4 orow[S];  // this lane's row of out, for Dvec in phase 1
+    {
+        RotBlock<D, E, FULL, 64, NT, 2> qk;
+        RowBlock<D, 64, NT> vb, db;
+        const char *const x[2] = {p.q + qoff, p.k + koff};
+        const int64_t xs[2] = {p.sq_s * 2, p.sk_s * 2};
+        qk.load(p, x, xs, s0, L, tid);
+        vb.load(p.v + ((int64_t)s0 * p.sv_s + (int64_t)head * p.sv_h) * 2, p.sv_s * 2, L, tid);
+        db.load(p.dout + ((int64_t)s0 * p.sdo_s + (int64_t)head * p.sdo_h) * 2, p.sdo_s * 2, L, tid);
+        const char *op = p.out + ((int64_t)(s0 + (rvalid ? row : 0)) * p.so_s + (int64_t)head * p.so_h) * 2;
+#pragma unroll
+        for (int t = 0; t < S; ++t) {
+            const int d0 = 16 * t + 8 * (lane >> 5);
+            orow[t] = (rvalid && d0 < D) ? *(const u32x4 *)(op + 2 * d0) : u32x4{0u, 0u, 0u, 0u};
+        }
+        // rows past the segment: lse = +inf makes their P (and dZ) zero
+        const float lv = tid < L ? p.lse[(int64_t)head * p.total + s0 + tid] * kLog2e : __builtin_inff();
+        char *const dst[2] = {lds + LDS::kQr, lds + LDS::kKr};
+        qk.store(dst, PTR, L, tid);
+        vb.store(lds + LDS::kV, PRD, tid);
+        db.store(lds + LDS::kDo, PTR, tid);
+        if (tid < 64) ((float *)(lds + LDS::kLse))[tid] = lv;
+    }
+    __syncthreads();
+
+    const float sl = p.scale_log2;
+    const uint32_t trl = tr_lane_offset<PTR>(lane);
+    const int ntile = (L + 31) >> 5;  // 32-row tiles of queries (and of keys)
+
+    // ---- phase 1: dQ for queries 32w..32w+31 -----------------------------------------
+    f32x16 dqacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = f32x16{};
+    {
+        u32x4 qop[S], dop[S];
+        float dot = 0.f;
+#pragma unroll
+        for (int t = 0; t < S; ++t) {
+            qop[t] = *(const u32x4 *)(lds + LDS::kQr + row * PTR + 32 * t + 16 * g);
+            dop[t] = *(const u32x4 *)(lds + LDS::kDo + row * PTR + 32 * t + 16 * g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {  // orow is zero past the row and the segment
+                dot = __builtin_fmaf(E::lo(orow[t][e]), E::lo(dop[t][e]), dot);
+                dot = __builtin_fmaf(E::hi(orow[t][e]), E::hi(dop[t][e]), dot);
+            }
+        }
+        const float dvq = sum_pair32(dot);  // rowsum(dO * O) of query `row`
+        if (g == 0) ((float *)(lds + LDS::kDvec))[row] = dvq;
+        const float lse2 = ((const float *)(lds + LDS::kLse))[row];
+        if (w < ntile) {  // uniform per wavefront
+            f32x16 sacc[2], dpacc[2];
+#pragma unroll
+            for (int a = 0; a < 2; ++a) {
+                sacc[a] = f32x16{};
+                dpacc[a] = f32x16{};
+                if (a < ntile) {
+#pragma unroll
+                    for (int t = 0; t < S; ++t)
+                        sacc[a] = E::mma(*(const u32x4 *)(lds + LDS::kKr + (32 * a + r) * PTR + 32 * t + 16 * g),
+                                         qop[t], sacc[a]);
+#pragma unroll
+                    for (int t = 0; t < S; ++t)
+                        dpacc[a] = E::mma(*(const u32x4 *)(lds + LDS::kV + (32 * a + r) * PRD + 32 * t + 16 * g),
+                                          dop[t], dpacc[a]);
+                }
+            }
+            u32x4 dsop[2][2];
+#pragma unroll
+            for (int a = 0; a < 2; ++a) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int key = 32 * a + 8 * (j >> 2) + 4 * g + (j & 3);
+                    const float pj = key < L ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[a][j], sl, -lse2)) : 0.f;
+                    sacc[a][j] = pj * (dpacc[a][j] - dvq);
+                }
+#pragma unroll
+                for (int h = 0; h < 2; ++h) dsop[a][h] = pack8<E>(sacc[a], h);
+            }
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+                for (int a = 0; a < 2; ++a) {
+                    if (a >= ntile) break;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        dqacc[dt] = E::mma(tr_operand<PTR>(lds + LDS::kKr, trl, a, h, dt), dsop[a][h], dqacc[dt]);
+                }
+            }
+        }
+    }
+    // Phase 2's B operands (this lane's key row of K_rot and V) before their
+    // LDS is reused.
+    u32x4 kop[S], vop[S];
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+        kop[t] = *(const u32x4 *)(lds + LDS::kKr + row * PTR + 32 * t + 16 * g);
+        vop[t] = *(const u32x4 *)(lds + LDS::kV + row * PRD + 32 * t + 16 * g);
+    }
+    __syncthreads();  // K_rot and V are dead; Dvec is complete
+    float *fq = (float *)(lds + LDS::kFq);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+            const int d0 = 32 * dt + 8 * jq + 4 * g;
+            if (d0 < D)
+                *(f32x4 *)(fq + row * (FP / 4) + d0) =
+                    f32x4{dqacc[dt][4 * jq + 0], dqacc[dt][4 * jq + 1], dqacc[dt][4 * jq + 2], dqacc[dt][4 * jq + 3]} *
+                    p.scale;
+        }
+    }
+
+    // ---- phase 2: dK, dV for keys 32w..32w+31 ----------------------------------------
+    f32x16 dvacc[NDT], dkacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+        dvacc[dt] = f32x16{};
+        dkacc[dt] = f32x16{};
+    }
+    if (w < ntile) {  // uniform per wavefront
+        const float *lsef = (const float *)(lds + LDS::kLse);
+        const float *dvf = (const float *)(lds + LDS::kDvec);
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            if (a >= ntile) break;
+            f32x16 sacc = f32x16{}, dpacc = f32x16{};
+#pragma unroll
+            for (int t = 0; t < S; ++t)
+                sacc = E::mma(*(const u32x4 *)(lds + LDS::kQr + (32 * a + r) * PTR + 32 * t + 16 * g), kop[t], sacc);
+#pragma unroll
+            for (int t = 0; t < S; ++t)
+                dpacc = E::mma(*(const u32x4 *)(lds + LDS::kDo + (32 * a + r) * PTR + 32 * t + 16 * g), vop[t], dpacc);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const f32x4 l4 = *(const f32x4 *)(lsef + 32 * a + 8 * m + 4 * g);
+                const f32x4 d4 = *(const f32x4 *)(dvf + 32 * a + 8 * m + 4 * g);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int j = 4 * m + i;
+                    const float pj = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j], sl, -l4[i]));
+                    sacc[j] = pj;
+                    dpacc[j] = pj * (dpacc[j] - d4[i]);
+                }
+            }
+            u32x4 pop[2], dsop[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                pop[h] = pack8<E>(sacc, h);
+                dsop[h] = pack8<E>(dpacc, h);
+            }
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    dvacc[dt] = E::mma(tr_operand<PTR>(lds + LDS::kDo, trl, a, h, dt), pop[h], dvacc[dt]);
+                    dkacc[dt] = E::mma(tr_operand<PTR>(lds + LDS::kQr, trl, a, h, dt), dsop[h], dkacc[dt]);
+                }
+            }
+        }
+    }
+    if (rvalid) {
+        char *dvr = p.dv + ((int64_t)(s0 + row) * p.sdv_s + (int64_t)head * p.sdv_h) * 2;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq) {
+                const int d0 = 32 * dt + 8 * jq + 4 * g;
+                if (d0 < D)
+                    *(u32x2 *)(dvr + 2 * d0) = u32x2{E::pack(dvacc[dt][4 * jq + 0], dvacc[dt][4 * jq + 1]),
+                                                     E::pack(dvacc[dt][4 * jq + 2], dvacc[dt][4 * jq + 3])};
+            }
+        }
+    }
+    __syncthreads();  // Q_rot and dO are dead
+    float *fk = (float *)(lds + LDS::kFk);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+            const int d0 = 32 * dt + 8 * jq + 4 * g;
+            if (d0 < D)
+                *(f32x4 *)(fk + row * (FP / 4) + d0) =
+                    f32x4{dkacc[dt][4 * jq + 0], dkacc[dt][4 * jq + 1], dkacc[dt][4 * jq + 2], dkacc[dt][4 * jq + 3]} *
+                    p.scale;
+        }
+    }
+    __syncthreads();
+    unrotate_store<D, E, FULL>(fq, FP / 4, p, p.dq + ((int64_t)s0 * p.sdq_s + (int64_t)head * p.sdq_h) * 2,
+                               p.sdq_s * 2, s0, L, tid, NT);
+    unrotate_store<D, E, FULL>(fk, FP / 4, p, p.dk + ((int64_t)s0 * p.sdk_s + (int64_t)head * p.sdk_h) * 2,
+                               p.sdk_s * 2, s0, L, tid, NT);
+}
+
 // ---- host-side dispatch -------------------------------------------------------------
 
 typedef void (*BwdFn)(BParams);
@@ -484,43 +830,42 @@ typedef void (*BwdFn)(BParams);
 struct BwdKernels {
     BwdFn dot, dq, dkdv;
     int nw;
+    BwdFn window;  // every segment <= 64 tokens: the one-pass kernel
 };
 
 template <int D, class E, bool FULL, int NW>
 BwdKernels bwd_kernels_nw() {
     return BwdKernels{(BwdFn)bwd_dot_kernel<D, E>, (BwdFn)bwd_dq_kernel<D, E, FULL, NW>,
-                      (BwdFn)bwd_dkdv_kernel<D, E, FULL, NW>, NW};
-}
-
-template <int D, class E, bool FULL>
-BwdKernels bwd_kernels_full(bool small) {
-    return small ? bwd_kernels_nw<D, E, FULL, 2>() : bwd_kernels_nw<D, E, FULL, 4>();
+                      (BwdFn)bwd_dkdv_kernel<D, E, FULL, NW>, NW, (BwdFn)bwd_window_kernel<D, E, FULL>};
 }
 
 template <int D, class E>
-BwdKernels bwd_kernels_e(bool full, bool small) {
-    return full ? bwd_kernels_full<D, E, true>(small) : bwd_kernels_full<D, E, false>(small);
+BwdKernels bwd_kernels_e(bool full) {
+    return full ? bwd_kernels_nw<D, E, true, 4>() : bwd_kernels_nw<D, E, false, 4>();
 }
 
 template <int D>
-BwdKernels bwd_kernels_d(int qkv, bool full, bool small) {
-    return qkv == FRA_DTYPE_BF16 ? bwd_kernels_e<D, BF16>(full, small) : bwd_kernels_e<D, F16>(full, small);
+BwdKernels bwd_kernels_d(int qkv, bool full) {
+    return qkv == FRA_DTYPE_BF16 ? bwd_kernels_e<D, BF16>(full) : bwd_kernels_e<D, F16>(full);
 }
 
-bool bwd_pick(int d, int qkv, bool full, bool small, BwdKernels &k) {
+bool bwd_pick(int d, int qkv, bool full, BwdKernels &k) {
     switch (d) {
-        case 64: k = bwd_kernels_d<64>(qkv, full, small); return true;
-        case 72: k = bwd_kernels_d<72>(qkv, full, small); return true;
-        case 80: k = bwd_kernels_d<80>(qkv, full, small); return true;
-        case 96: k = bwd_kernels_d<96>(qkv, full, small); return true;
-        case 128: k = bwd_kernels_d<128>(qkv, full, small); return true;
+        case 64: k = bwd_kernels_d<64>(qkv, full); return true;
+        case 72: k = bwd_kernels_d<72>(qkv, full); return true;
+        case 80: k = bwd_kernels_d<80>(qkv, full); return true;
+        case 96: k = bwd_kernels_d<96>(qkv, full); return true;
+        case 128: k = bwd_kernels_d<128>(qkv, full); return true;
         default: return false;
     }
 }
 
 bool aligned_to(const void *ptr, int bytes) { return ((uintptr_t)ptr % (uintptr_t)bytes) == 0; }
 
-int64_t bwd_ws_bytes(const fra_bwd_args *a) { return (int64_t)a->num_heads * a->total_seq * 4; }
+// Scratch of the two-kernel path (Dvec); the one-pass window kernel needs none.
+int64_t bwd_ws_bytes(const fra_bwd_args *a) {
+    return a->max_seqlen <= 64 ? 0 : (int64_t)a->num_heads * a->total_seq * 4;
+}
 
 int bwd_check(const fra_bwd_args *a) {
     if (!a) return fra_fail(FRA_EINVAL, "args is NULL");
@@ -552,7 +897,7 @@ int bwd_check(const fra_bwd_args *a) {
     for (int i = 0; i < 17; ++i)
         if (st[i] < 0) return fra_fail(FRA_EINVAL, "strides must be >= 0");
     BwdKernels k;
-    if (!bwd_pick(d, a->qkv_dtype, a->rope_width == d, true, k))
+    if (!bwd_pick(d, a->qkv_dtype, a->rope_width == d, k))
         return fra_fail(FRA_EUNSUPPORTED, "head_dim=%d has no compiled kernel (built: 64, 72, 80, 96, 128)", d);
     if (a->rope_dtype != FRA_DTYPE_F32)
         return fra_fail(FRA_EUNSUPPORTED, "the backward takes float32 cos/sin tables, got %s",
@@ -589,12 +934,12 @@ int fra_bwd_varlen(const fra_bwd_args *a, void *stream) {
     int rc = bwd_check(a);
     if (rc != FRA_OK) return rc;
     if (a->total_seq == 0) return fra_fail(FRA_OK, "%s", "");
-    if (!a->workspace || a->workspace_bytes < bwd_ws_bytes(a) || !aligned_to(a->workspace, 16))
+    if (bwd_ws_bytes(a) > 0 && (!a->workspace || a->workspace_bytes < bwd_ws_bytes(a) || !aligned_to(a->workspace, 16)))
         return fra_fail(FRA_EINVAL, "workspace must be 16-byte aligned and hold at least %lld bytes",
                         (long long)bwd_ws_bytes(a));
     const int d = a->head_dim;
     BwdKernels k;
-    bwd_pick(d, a->qkv_dtype, a->rope_width == d, a->max_seqlen <= 64, k);
+    bwd_pick(d, a->qkv_dtype, a->rope_width == d, k);
 
     BParams p;
     memset(&p, 0, sizeof(p));
@@ -637,6 +982,15 @@ int fra_bwd_varlen(const fra_bwd_args *a, void *stream) {
     const hipStream_t st = (hipStream_t)stream;
     const int64_t rows = (int64_t)a->total_seq * a->num_heads;
     const int64_t sh = (int64_t)a->num_seqs * a->num_heads;
+    if (a->max_seqlen <= 64) {
+        if (sh > 0x7fffffff) return fra_fail(FRA_EUNSUPPORTED, "grid of %lld workgroups is too large", (long long)sh);
+        p.blocks = 1;
+        hipLaunchKernelGGL(k.window, dim3((unsigned)sh), dim3(128), 0, st, p);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess)
+            return fra_fail(FRA_EHIP, "launch of the window backward kernel failed: %s", hipGetErrorString(e));
+        return fra_fail(FRA_OK, "%s", "");
+    }
     const int rows_per_wg = 32 * k.nw;
     const int64_t blocks = (a->max_seqlen + rows_per_wg - 1) / rows_per_wg;
     const int64_t grid_dot = (rows + 255) / 256, grid = sh * blocks;

@@ -171,8 +171,12 @@ def test_bwd_struct_and_workspace_size():
     lib = _lib.load()
     assert lib.fra_sizeof_bwd_args() == ctypes.sizeof(_lib.BwdArgs)
     nbytes = ctypes.c_int64(-1)
-    assert lib.fra_bwd_workspace_bytes(make_bwd_args(n=9216, h=16), ctypes.byref(nbytes)) == _lib.FRA_OK
+    a = make_bwd_args(n=9216, h=16, max_seqlen=9216, nseg=1)
+    assert lib.fra_bwd_workspace_bytes(a, ctypes.byref(nbytes)) == _lib.FRA_OK
     assert nbytes.value == 9216 * 16 * 4  # one fp32 per (head, token): the rows' dout . out
+    # segments of at most 64 tokens take the one-pass kernel, which needs no scratch
+    assert lib.fra_bwd_workspace_bytes(make_bwd_args(n=9216, nseg=144), ctypes.byref(nbytes)) == _lib.FRA_OK
+    assert nbytes.value == 0
     # total_seq == 0 validates and returns without launching (no workspace needed)
     assert lib.fra_bwd_varlen(make_bwd_args(n=0), None) == _lib.FRA_OK
 
@@ -201,7 +205,7 @@ def test_bwd_validation_errors(field, value, code, msg):
 
 def test_bwd_requires_workspace():
     lib = _lib.load()
-    a = make_bwd_args()
+    a = make_bwd_args(max_seqlen=1000, nseg=1)
     assert lib.fra_bwd_varlen(a, None) == _lib.FRA_EINVAL  # no workspace: fails before any launch
     assert "workspace" in lib.fra_last_error().decode()
     a.workspace, a.workspace_bytes = (1 << 20) * 20, 1024 * 16 * 4 - 4
