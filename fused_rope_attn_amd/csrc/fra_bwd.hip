@@ -54,7 +54,7 @@ struct BParams {
     int64_t sq_s, sq_h, sk_s, sk_h, sv_s, sv_h, so_s, so_h, sdo_s, sdo_h;
     int64_t sdq_s, sdq_h, sdk_s, sdk_h, sdv_s, sdv_h, sr_s;
     int32_t total, num_heads, num_seqs;
-    int32_t blocks;    // row blocks per (segment, head) of the launched kernel
+    int32_t blocks;    // row blocks per (segment, head) of the dq and dk/dv units
     float scale;       // softmax_scale
     float scale_log2;  // softmax_scale * log2(e)
 };
@@ -292,20 +292,25 @@ __device__ __forceinline__ u32x4 pack8(const f32x16 &x, int h) {
 
 // ---- dq -------------------------------------------------------------------------
 
+template <int D, int NW> struct DqLds {
+    static constexpr int PTR = bwd_pitch_tr(D), PRD = bwd_pitch_rows(D), FP = bwd_pitch_f32(D);
+    static constexpr int BQ = 32 * NW, BKV = kBwdBlockKV;
+    static constexpr int kKr = 0, kV = BKV * PTR;
+    static constexpr int kStage = kV + BKV * PRD;
+    static constexpr int kQ = BQ * PRD, kF = BQ * FP;
+    static constexpr int kBytes = cmax(kStage, cmax(kQ, kF));
+};
+
+// dq of one unit (segment, head, block of 32*NW queries).
 template <int D, class E, bool FULL, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(BwdOcc<D>::kWaves, BwdOcc<D>::kWaves)))
-void bwd_dq_kernel(const BParams p) {
+__device__ __forceinline__ void bwd_dq_unit(const BParams &p, char *lds, int unit) {
+    using LDS = DqLds<D, NW>;
     constexpr int DP = bwd_dp(D), S = DP / 16, NDT = (D + 31) / 32;
-    constexpr int PTR = bwd_pitch_tr(D), PRD = bwd_pitch_rows(D), FP = bwd_pitch_f32(D);
-    constexpr int BQ = 32 * NW, BKV = kBwdBlockKV, NT = 64 * NW;
-    constexpr int kKr = 0, kV = BKV * PTR;
-    constexpr int kStage = kV + BKV * PRD;
-    constexpr int kQ = BQ * PRD, kF = BQ * FP;
-    constexpr int kBytes = cmax(kStage, cmax(kQ, kF));
-    __shared__ __attribute__((aligned(16))) char lds[kBytes];
+    constexpr int PTR = LDS::PTR, PRD = LDS::PRD, FP = LDS::FP;
+    constexpr int BQ = LDS::BQ, BKV = LDS::BKV, NT = 64 * NW;
+    constexpr int kKr = LDS::kKr, kV = LDS::kV;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 31, g = lane >> 5;
-    const int unit = xcd_remap(blockIdx.x, gridDim.x);
     const int sh = unit / p.blocks, qb = unit - sh * p.blocks;
     const int seg = sh / p.num_heads, head = sh - seg * p.num_heads;
     int s0, L;
@@ -345,24 +350,32 @@ void bwd_dq_kernel(const BParams p) {
     for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = f32x16{};
     const uint32_t trl = tr_lane_offset<PTR>(lane);
     const int nkb = (L + BKV - 1) / BKV;
+    // Key blocks through registers, one block ahead: block kb + 1's loads are
+    // in flight while block kb is computed.
+    RotBlock<D, E, FULL, BKV, NT, 1> kbk;
+    RowBlock<D, BKV, NT> vbk;
+    auto load_block = [&](int kb) {
+        const int k0 = kb * BKV, nk = min(BKV, L - k0);
+        const char *const xk[1] = {p.k + ((int64_t)(s0 + k0) * p.sk_s + (int64_t)head * p.sk_h) * 2};
+        const int64_t xs[1] = {p.sk_s * 2};
+        // an opaque thread id: the items' addresses are recomputed per block
+        // instead of being kept live across the loop
+        const int ft = fresh(tid);
+        kbk.load(p, xk, xs, s0 + k0, nk, ft);
+        vbk.load(p.v + ((int64_t)(s0 + k0) * p.sv_s + (int64_t)head * p.sv_h) * 2, p.sv_s * 2, nk, ft);
+    };
+    load_block(0);
     for (int kb = 0; kb < nkb; ++kb) {
         const int k0 = kb * BKV, nk = min(BKV, L - k0);
+        __syncthreads();  // the previous block's (or Q's) LDS reads are done
         {
-            RotBlock<D, E, FULL, BKV, NT, 1> kbk;
-            RowBlock<D, BKV, NT> vbk;
-            const char *const xk[1] = {p.k + ((int64_t)(s0 + k0) * p.sk_s + (int64_t)head * p.sk_h) * 2};
-            const int64_t xs[1] = {p.sk_s * 2};
-            // an opaque thread id: the items' addresses are recomputed per
-            // block instead of being kept live across the loop
             const int ft = fresh(tid);
-            kbk.load(p, xk, xs, s0 + k0, nk, ft);
-            vbk.load(p.v + ((int64_t)(s0 + k0) * p.sv_s + (int64_t)head * p.sv_h) * 2, p.sv_s * 2, nk, ft);
-            __syncthreads();  // the previous block's (or Q's) LDS reads are done
             char *const dst[1] = {lds + kKr};
             kbk.store(dst, PTR, nk, ft);
             vbk.store(lds + kV, PRD, ft);
         }
         __syncthreads();
+        if (kb + 1 < nkb) load_block(kb + 1);
         // S^T = K_rot Q_rot^T and dP^T = V dout^T: rows key, column query.
         f32x16 sacc[2], dpacc[2];
 #pragma unroll
@@ -422,20 +435,25 @@ void bwd_dq_kernel(const BParams p) {
 
 // ---- dk, dv -----------------------------------------------------------------------
 
+template <int D, int NW> struct DkdvLds {
+    static constexpr int PTR = bwd_pitch_tr(D), PRD = bwd_pitch_rows(D), FP = bwd_pitch_f32(D);
+    static constexpr int BKV = 32 * NW, BQ = kBwdBlockQ;
+    static constexpr int kQr = 0, kDo = BQ * PTR, kLse = kDo + BQ * PTR, kDv = kLse + BQ * 4;
+    static constexpr int kStage = kDv + BQ * 4;
+    static constexpr int kK = BKV * PRD, kF = BKV * FP;
+    static constexpr int kBytes = cmax(kStage, cmax(kK, kF));
+};
+
+// dk and dv of one unit (segment, head, block of 32*NW keys).
 template <int D, class E, bool FULL, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(BwdOcc<D>::kWaves, BwdOcc<D>::kWaves)))
-void bwd_dkdv_kernel(const BParams p) {
+__device__ __forceinline__ void bwd_dkdv_unit(const BParams &p, char *lds, int unit) {
+    using LDS = DkdvLds<D, NW>;
     constexpr int DP = bwd_dp(D), S = DP / 16, NDT = (D + 31) / 32;
-    constexpr int PTR = bwd_pitch_tr(D), PRD = bwd_pitch_rows(D), FP = bwd_pitch_f32(D);
-    constexpr int BKV = 32 * NW, BQ = kBwdBlockQ, NT = 64 * NW;
-    constexpr int kQr = 0, kDo = BQ * PTR, kLse = kDo + BQ * PTR, kDv = kLse + BQ * 4;
-    constexpr int kStage = kDv + BQ * 4;
-    constexpr int kK = BKV * PRD, kF = BKV * FP;
-    constexpr int kBytes = cmax(kStage, cmax(kK, kF));
-    __shared__ __attribute__((aligned(16))) char lds[kBytes];
+    constexpr int PTR = LDS::PTR, PRD = LDS::PRD, FP = LDS::FP;
+    constexpr int BKV = LDS::BKV, BQ = LDS::BQ, NT = 64 * NW;
+    constexpr int kQr = LDS::kQr, kDo = LDS::kDo, kLse = LDS::kLse, kDv = LDS::kDv;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 31, g = lane >> 5;
-    const int unit = xcd_remap(blockIdx.x, gridDim.x);
     const int sh = unit / p.blocks, kb = unit - sh * p.blocks;
     const int seg = sh / p.num_heads, head = sh - seg * p.num_heads;
     int s0, L;
@@ -476,35 +494,51 @@ void bwd_dkdv_kernel(const BParams p) {
     const float *lsef = (const float *)(lds + kLse);
     const float *dvf = (const float *)(lds + kDv);
     const int nqb = (L + BQ - 1) / BQ;
+    // Query blocks through registers, one block ahead: block qb + 1's loads
+    // are in flight while block qb is computed.  Full-width tables (twice the
+    // table registers) would spill that way: they load each block at the top
+    // of its own iteration.
+    constexpr bool AHEAD = !FULL;
+    RotBlock<D, E, FULL, BQ, NT, 1> qbk;
+    RowBlock<D, BQ, NT> dbk;
+    float lv, dvv;
+    auto load_block = [&](int qb) {
+        const int q0 = qb * BQ, nq = min(BQ, L - q0);
+        const char *const xq[1] = {p.q + ((int64_t)(s0 + q0) * p.sq_s + (int64_t)head * p.sq_h) * 2};
+        const int64_t xs[1] = {p.sq_s * 2};
+        // an opaque thread id: the items' addresses are recomputed per block
+        // instead of being kept live across the loop
+        const int ft = fresh(tid);
+        qbk.load(p, xq, xs, s0 + q0, nq, ft);
+        dbk.load(p.dout + ((int64_t)(s0 + q0) * p.sdo_s + (int64_t)head * p.sdo_h) * 2, p.sdo_s * 2, nq, ft);
+        // Rows past the segment: lse = +inf makes their P (and dZ) zero.
+        lv = __builtin_inff();
+        dvv = 0.f;
+        if (ft < nq) {
+            const int64_t srow = (int64_t)head * p.total + s0 + q0 + ft;
+            lv = p.lse[srow] * kLog2e;
+            dvv = p.dvec[srow];
+        }
+    };
+    if constexpr (AHEAD) load_block(0);
     for (int qb = 0; qb < nqb; ++qb) {
         const int q0 = qb * BQ, nq = min(BQ, L - q0);
+        if constexpr (!AHEAD) load_block(qb);
+        __syncthreads();  // the previous block's (or K's) LDS reads are done
         {
-            RotBlock<D, E, FULL, BQ, NT, 1> qbk;
-            RowBlock<D, BQ, NT> dbk;
-            const char *const xq[1] = {p.q + ((int64_t)(s0 + q0) * p.sq_s + (int64_t)head * p.sq_h) * 2};
-            const int64_t xs[1] = {p.sq_s * 2};
-            // an opaque thread id: the items' addresses are recomputed per
-            // block instead of being kept live across the loop
             const int ft = fresh(tid);
-            qbk.load(p, xq, xs, s0 + q0, nq, ft);
-            dbk.load(p.dout + ((int64_t)(s0 + q0) * p.sdo_s + (int64_t)head * p.sdo_h) * 2, p.sdo_s * 2, nq, ft);
-            // Rows past the segment: lse = +inf makes their P (and dZ) zero.
-            float lv = __builtin_inff(), dvv = 0.f;
-            if (tid < nq) {
-                const int64_t srow = (int64_t)head * p.total + s0 + q0 + tid;
-                lv = p.lse[srow] * kLog2e;
-                dvv = p.dvec[srow];
-            }
-            __syncthreads();  // the previous block's (or K's) LDS reads are done
             char *const dst[1] = {lds + kQr};
             qbk.store(dst, PTR, nq, ft);
             dbk.store(lds + kDo, PTR, ft);
-            if (tid < BQ) {
-                ((float *)(lds + kLse))[tid] = lv;
-                ((float *)(lds + kDv))[tid] = dvv;
+            if (ft < BQ) {
+                ((float *)(lds + kLse))[ft] = lv;
+                ((float *)(lds + kDv))[ft] = dvv;
             }
         }
         __syncthreads();
+        if constexpr (AHEAD) {
+            if (qb + 1 < nqb) load_block(qb + 1);
+        }
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
             if (32 * a >= nq) break;  // uniform
@@ -579,6 +613,22 @@ void bwd_dkdv_kernel(const BParams p) {
     __syncthreads();
     unrotate_store<D, E, FULL>(f, FP / 4, p, p.dk + ((int64_t)(s0 + k0) * p.sdk_s + (int64_t)head * p.sdk_h) * 2,
                                p.sdk_s * 2, s0 + k0, nk, tid, NT);
+}
+
+// The dq and dk/dv units of a call in one launch: logical unit 2u is the
+// dk/dv unit u, 2u + 1 the dq unit u (same segment, head and block, so the
+// pair shares its q, k, v and dout lines in one XCD's L2, and every XCD gets
+// both kinds).  One grid of both leaves one partly filled last round of
+// workgroups instead of two.
+template <int D, class E, bool FULL, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(BwdOcc<D>::kWaves, BwdOcc<D>::kWaves)))
+void bwd_long_kernel(const BParams p) {
+    __shared__ __attribute__((aligned(16))) char lds[cmax(DqLds<D, NW>::kBytes, DkdvLds<D, NW>::kBytes)];
+    const int b = xcd_remap(blockIdx.x, gridDim.x);
+    if ((b & 1) == 0)
+        bwd_dkdv_unit<D, E, FULL, NW>(p, lds, b >> 1);
+    else
+        bwd_dq_unit<D, E, FULL, NW>(p, lds, b >> 1);
 }
 
 // ---- window layers: the whole backward of one (segment, head) in one pass -------------
@@ -828,15 +878,15 @@ void bwd_window_kernel(const BParams p) {
 typedef void (*BwdFn)(BParams);
 
 struct BwdKernels {
-    BwdFn dot, dq, dkdv;
+    BwdFn dot, matrix;  // longer segments: Dvec, then dq and dk/dv units in one launch
     int nw;
     BwdFn window;  // every segment <= 64 tokens: the one-pass kernel
 };
 
 template <int D, class E, bool FULL, int NW>
 BwdKernels bwd_kernels_nw() {
-    return BwdKernels{(BwdFn)bwd_dot_kernel<D, E>, (BwdFn)bwd_dq_kernel<D, E, FULL, NW>,
-                      (BwdFn)bwd_dkdv_kernel<D, E, FULL, NW>, NW, (BwdFn)bwd_window_kernel<D, E, FULL>};
+    return BwdKernels{(BwdFn)bwd_dot_kernel<D, E>, (BwdFn)bwd_long_kernel<D, E, FULL, NW>, NW,
+                      (BwdFn)bwd_window_kernel<D, E, FULL>};
 }
 
 template <int D, class E>
@@ -993,19 +1043,16 @@ int fra_bwd_varlen(const fra_bwd_args *a, void *stream) {
     }
     const int rows_per_wg = 32 * k.nw;
     const int64_t blocks = (a->max_seqlen + rows_per_wg - 1) / rows_per_wg;
-    const int64_t grid_dot = (rows + 255) / 256, grid = sh * blocks;
+    const int64_t grid_dot = (rows + 255) / 256, units = sh * blocks, grid = 2 * units;
     if (grid_dot > 0x7fffffff || grid > 0x7fffffff)
         return fra_fail(FRA_EUNSUPPORTED, "grid of %lld workgroups is too large", (long long)std::max(grid, grid_dot));
     p.blocks = (int32_t)blocks;
     hipLaunchKernelGGL(k.dot, dim3((unsigned)grid_dot), dim3(256), 0, st, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fra_fail(FRA_EHIP, "launch of the backward row dot products failed: %s", hipGetErrorString(e));
-    hipLaunchKernelGGL(k.dq, dim3((unsigned)grid), dim3(64 * k.nw), 0, st, p);
+    hipLaunchKernelGGL(k.matrix, dim3((unsigned)grid), dim3(64 * k.nw), 0, st, p);
     e = hipGetLastError();
-    if (e != hipSuccess) return fra_fail(FRA_EHIP, "launch of the dq kernel failed: %s", hipGetErrorString(e));
-    hipLaunchKernelGGL(k.dkdv, dim3((unsigned)grid), dim3(64 * k.nw), 0, st, p);
-    e = hipGetLastError();
-    if (e != hipSuccess) return fra_fail(FRA_EHIP, "launch of the dk/dv kernel failed: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return fra_fail(FRA_EHIP, "launch of the dq / dk,dv kernel failed: %s", hipGetErrorString(e));
     return fra_fail(FRA_OK, "%s", "");
 }
 
