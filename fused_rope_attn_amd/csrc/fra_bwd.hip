@@ -295,10 +295,11 @@ __device__ __forceinline__ u32x4 pack8(const f32x16 &x, int h) {
 template <int D, int NW> struct DqLds {
     static constexpr int PTR = bwd_pitch_tr(D), PRD = bwd_pitch_rows(D), FP = bwd_pitch_f32(D);
     static constexpr int BQ = 32 * NW, BKV = kBwdBlockKV;
+    // Two stages (key block kb in stage kb & 1), each K_rot then V.
     static constexpr int kKr = 0, kV = BKV * PTR;
     static constexpr int kStage = kV + BKV * PRD;
     static constexpr int kQ = BQ * PRD, kF = BQ * FP;
-    static constexpr int kBytes = cmax(kStage, cmax(kQ, kF));
+    static constexpr int kBytes = cmax(2 * kStage, cmax(kQ, kF));
 };
 
 // dq of one unit (segment, head, block of 32*NW queries).
@@ -364,18 +365,29 @@ __device__ __forceinline__ void bwd_dq_unit(const BParams &p, char *lds, int uni
         kbk.load(p, xk, xs, s0 + k0, nk, ft);
         vbk.load(p.v + ((int64_t)(s0 + k0) * p.sv_s + (int64_t)head * p.sv_h) * 2, p.sv_s * 2, nk, ft);
     };
+    // Block kb goes to LDS stage kb & 1 at the start of iteration kb - 1, so
+    // a wavefront that is ahead stores the next block while the others still
+    // read the current one; one barrier per block.
+    auto store_block = [&](int kb) {
+        const int nk = min(BKV, L - kb * BKV);
+        const int ft = fresh(tid);
+        char *const base = lds + (kb & 1) * LDS::kStage;
+        char *const dst[1] = {base + kKr};
+        kbk.store(dst, PTR, nk, ft);
+        vbk.store(base + kV, PRD, ft);
+    };
     load_block(0);
+    __syncthreads();  // Q_rot's rows are in registers: stage 0 may go over them
+    store_block(0);
+    if (nkb > 1) load_block(1);
+    __syncthreads();
     for (int kb = 0; kb < nkb; ++kb) {
         const int k0 = kb * BKV, nk = min(BKV, L - k0);
-        __syncthreads();  // the previous block's (or Q's) LDS reads are done
-        {
-            const int ft = fresh(tid);
-            char *const dst[1] = {lds + kKr};
-            kbk.store(dst, PTR, nk, ft);
-            vbk.store(lds + kV, PRD, ft);
+        if (kb + 1 < nkb) {
+            store_block(kb + 1);  // the other stage: its last reader (block kb - 1) passed the barrier
+            if (kb + 2 < nkb) load_block(kb + 2);
         }
-        __syncthreads();
-        if (kb + 1 < nkb) load_block(kb + 1);
+        const char *const stage = lds + (kb & 1) * LDS::kStage;
         // S^T = K_rot Q_rot^T and dP^T = V dout^T: rows key, column query.
         f32x16 sacc[2], dpacc[2];
 #pragma unroll
@@ -384,10 +396,10 @@ __device__ __forceinline__ void bwd_dq_unit(const BParams &p, char *lds, int uni
             dpacc[a] = f32x16{};
 #pragma unroll
             for (int t = 0; t < S; ++t)
-                sacc[a] = E::mma(*(const u32x4 *)(lds + kKr + (32 * a + r) * PTR + 32 * t + 16 * g), qop[t], sacc[a]);
+                sacc[a] = E::mma(*(const u32x4 *)(stage + kKr + (32 * a + r) * PTR + 32 * t + 16 * g), qop[t], sacc[a]);
 #pragma unroll
             for (int t = 0; t < S; ++t)
-                dpacc[a] = E::mma(*(const u32x4 *)(lds + kV + (32 * a + r) * PRD + 32 * t + 16 * g), dop[t], dpacc[a]);
+                dpacc[a] = E::mma(*(const u32x4 *)(stage + kV + (32 * a + r) * PRD + 32 * t + 16 * g), dop[t], dpacc[a]);
         }
         // dZ^T = P^T * (dP^T - Dvec), keys past the segment masked.
         u32x4 dsop[2][2];
@@ -409,13 +421,14 @@ __device__ __forceinline__ void bwd_dq_unit(const BParams &p, char *lds, int uni
             for (int a = 0; a < 2; ++a) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
-                    dqacc[dt] = E::mma(tr_operand<PTR>(lds + kKr, trl, a, h, dt), dsop[a][h], dqacc[dt]);
+                    dqacc[dt] = E::mma(tr_operand<PTR>(stage + kKr, trl, a, h, dt), dsop[a][h], dqacc[dt]);
             }
         }
+        __syncthreads();  // block kb + 1's stage is written; block kb's is read
     }
 
-    // dQ_rot rows (fp32, scaled) through LDS, then the inverse rotation.
-    __syncthreads();
+    // dQ_rot rows (fp32, scaled) through LDS (free after the loop's last
+    // barrier), then the inverse rotation.
     float *f = (float *)lds;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
@@ -438,10 +451,11 @@ __device__ __forceinline__ void bwd_dq_unit(const BParams &p, char *lds, int uni
 template <int D, int NW> struct DkdvLds {
     static constexpr int PTR = bwd_pitch_tr(D), PRD = bwd_pitch_rows(D), FP = bwd_pitch_f32(D);
     static constexpr int BKV = 32 * NW, BQ = kBwdBlockQ;
+    // Two stages (query block qb in stage qb & 1), each Q_rot, dO, lse, Dvec.
     static constexpr int kQr = 0, kDo = BQ * PTR, kLse = kDo + BQ * PTR, kDv = kLse + BQ * 4;
     static constexpr int kStage = kDv + BQ * 4;
     static constexpr int kK = BKV * PRD, kF = BKV * FP;
-    static constexpr int kBytes = cmax(kStage, cmax(kK, kF));
+    static constexpr int kBytes = cmax(2 * kStage, cmax(kK, kF));
 };
 
 // dk and dv of one unit (segment, head, block of 32*NW keys).
@@ -491,8 +505,6 @@ __device__ __forceinline__ void bwd_dkdv_unit(const BParams &p, char *lds, int u
         dkacc[dt] = f32x16{};
     }
     const uint32_t trl = tr_lane_offset<PTR>(lane);
-    const float *lsef = (const float *)(lds + kLse);
-    const float *dvf = (const float *)(lds + kDv);
     const int nqb = (L + BQ - 1) / BQ;
     // Query blocks through registers, one block ahead: block qb + 1's loads
     // are in flight while block qb is computed.  Full-width tables (twice the
@@ -520,25 +532,40 @@ __device__ __forceinline__ void bwd_dkdv_unit(const BParams &p, char *lds, int u
             dvv = p.dvec[srow];
         }
     };
-    if constexpr (AHEAD) load_block(0);
+    // Block qb goes to LDS stage qb & 1 at the start of iteration qb - 1, so
+    // a wavefront that is ahead stores the next block while the others still
+    // read the current one; one barrier per block.
+    auto store_block = [&](int qb) {
+        const int nq = min(BQ, L - qb * BQ);
+        const int ft = fresh(tid);
+        char *const base = lds + (qb & 1) * LDS::kStage;
+        char *const dst[1] = {base + kQr};
+        qbk.store(dst, PTR, nq, ft);
+        dbk.store(base + kDo, PTR, ft);
+        if (ft < BQ) {
+            ((float *)(base + kLse))[ft] = lv;
+            ((float *)(base + kDv))[ft] = dvv;
+        }
+    };
+    load_block(0);
+    __syncthreads();  // K_rot's rows are in registers: stage 0 may go over them
+    store_block(0);
+    if constexpr (AHEAD) {
+        if (nqb > 1) load_block(1);
+    }
+    __syncthreads();
     for (int qb = 0; qb < nqb; ++qb) {
         const int q0 = qb * BQ, nq = min(BQ, L - q0);
-        if constexpr (!AHEAD) load_block(qb);
-        __syncthreads();  // the previous block's (or K's) LDS reads are done
-        {
-            const int ft = fresh(tid);
-            char *const dst[1] = {lds + kQr};
-            qbk.store(dst, PTR, nq, ft);
-            dbk.store(lds + kDo, PTR, ft);
-            if (ft < BQ) {
-                ((float *)(lds + kLse))[ft] = lv;
-                ((float *)(lds + kDv))[ft] = dvv;
+        if (qb + 1 < nqb) {
+            if constexpr (!AHEAD) load_block(qb + 1);
+            store_block(qb + 1);  // the other stage: its last reader (block qb - 1) passed the barrier
+            if constexpr (AHEAD) {
+                if (qb + 2 < nqb) load_block(qb + 2);
             }
         }
-        __syncthreads();
-        if constexpr (AHEAD) {
-            if (qb + 1 < nqb) load_block(qb + 1);
-        }
+        const char *const stage = lds + (qb & 1) * LDS::kStage;
+        const float *lsef = (const float *)(stage + kLse);
+        const float *dvf = (const float *)(stage + kDv);
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
             if (32 * a >= nq) break;  // uniform
@@ -546,10 +573,10 @@ __device__ __forceinline__ void bwd_dkdv_unit(const BParams &p, char *lds, int u
             f32x16 sacc = f32x16{}, dpacc = f32x16{};
 #pragma unroll
             for (int t = 0; t < S; ++t)
-                sacc = E::mma(*(const u32x4 *)(lds + kQr + (32 * a + r) * PTR + 32 * t + 16 * g), kop[t], sacc);
+                sacc = E::mma(*(const u32x4 *)(stage + kQr + (32 * a + r) * PTR + 32 * t + 16 * g), kop[t], sacc);
 #pragma unroll
             for (int t = 0; t < S; ++t)
-                dpacc = E::mma(*(const u32x4 *)(lds + kDo + (32 * a + r) * PTR + 32 * t + 16 * g), vop[t], dpacc);
+                dpacc = E::mma(*(const u32x4 *)(stage + kDo + (32 * a + r) * PTR + 32 * t + 16 * g), vop[t], dpacc);
             // Element j holds query 32a + 8(j/4) + 4g + (j%4).
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
@@ -574,11 +601,12 @@ __device__ __forceinline__ void bwd_dkdv_unit(const BParams &p, char *lds, int u
             for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    dvacc[dt] = E::mma(tr_operand<PTR>(lds + kDo, trl, a, h, dt), pop[h], dvacc[dt]);
-                    dkacc[dt] = E::mma(tr_operand<PTR>(lds + kQr, trl, a, h, dt), dsop[h], dkacc[dt]);
+                    dvacc[dt] = E::mma(tr_operand<PTR>(stage + kDo, trl, a, h, dt), pop[h], dvacc[dt]);
+                    dkacc[dt] = E::mma(tr_operand<PTR>(stage + kQr, trl, a, h, dt), dsop[h], dkacc[dt]);
                 }
             }
         }
+        __syncthreads();  // block qb + 1's stage is written; block qb's is read
     }
 
     // dV rows straight from the accumulators (lane (r, g): key ki, d = 32dt +
