@@ -178,3 +178,31 @@ def test_backward_identities_full_size(device, nseg, L, h):
     sdk = _segment_sums(dk, cu)
     dk_row = float(dk.double().abs().mean())
     assert float(sdk.abs().mean()) <= 0.05 * dk_row * math.sqrt(L), (float(sdk.abs().mean()), dk_row)
+
+
+@pytest.mark.parametrize("lens,d", [([64, 64, 30], 80), ([300, 40], 72)])
+def test_autograd_packed_qkv_views(device, lens, d):
+    """HF's `qkv(x).reshape(n, 3, h, d).unbind(1)` views (non-contiguous,
+    read in place): the gradient reaches the packed tensor and equals the
+    gradient of contiguous inputs bit for bit."""
+    c = on(make_case(lens, 2, d, seed=640), device)
+    qkv = torch.stack([c["q"], c["k"], c["v"]], 1).requires_grad_(True)  # [n, 3, h, d]
+    q, k, v = qkv.unbind(1)
+    assert not q.is_contiguous()
+    out = fused_rope_attention(q, k, v, c["cos"], c["sin"], c["cu"], c["max_seqlen"])
+    out.backward(c["dout"])
+    _, _, dq, dk, dv = gpu_fwd_bwd(c)
+    torch.cuda.synchronize()
+    assert torch.equal(qkv.grad[:, 0], dq) and torch.equal(qkv.grad[:, 1], dk) and torch.equal(qkv.grad[:, 2], dv)
+
+
+def test_backward_bf16_tables_widened(device):
+    """bf16 tables: the backward widens them to fp32 (exact), so the
+    gradients equal those computed with the widened tables."""
+    c = on(make_case([200, 64], 2, 80, seed=650), device)
+    cb = dict(c, cos=c["cos"].to(torch.bfloat16), sin=c["sin"].to(torch.bfloat16))
+    cf = dict(c, cos=cb["cos"].float(), sin=cb["sin"].float())
+    a = gpu_fwd_bwd(cb)
+    b = gpu_fwd_bwd(cf)
+    for x, y in zip(a[2:], b[2:]):
+        assert torch.equal(x, y)
