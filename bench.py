@@ -202,6 +202,53 @@ def run_workload(name: str, steps: int, warmup: int, flush: torch.Tensor, dev) -
             "warm_achieved": (nbytes if hbm else flops) / (m["warm_us"] * 1e-6) / (1e9 if hbm else 1e12)}, inp
 
 
+def unfused_call(inp):
+    """A closure running the unfused path on the GPU, as the reference's own
+    benchmark baseline does it (bench.py:72-82 of the reference: rotate Q and
+    K with separate elementwise ops in fp32, round to the input dtype, then
+    varlen attention), with torch's ``varlen_attn`` in place of the CUDA-only
+    flash-attn."""
+    from torch.nn.attention.varlen import varlen_attn
+    q, k, v, cos, sin, cu = (inp[x] for x in ("q", "k", "v", "cos", "sin", "cu_seqlens"))
+    ms = inp["max_seqlen"]
+    half = q.shape[2] // 2
+    c, s = cos.float()[:, None, :], sin.float()[:, None, :]
+
+    def rot(x):
+        xf = x.float()
+        x0, x1 = xf[..., :half], xf[..., half:]
+        return torch.cat([x0 * c - x1 * s, x0 * s + x1 * c], -1).to(x.dtype)
+
+    def call():
+        return varlen_attn(rot(q), rot(k), v, cu, cu, ms, ms)
+
+    return call
+
+
+def run_comparator(name: str, steps: int, warmup: int, flush: torch.Tensor, dev) -> dict:
+    """The fused op and the unfused torch path on the same inputs and GPU:
+    cold medians and their ratio (context only; the reference's published
+    figures are this ratio on its own hardware)."""
+    w = WORKLOADS[name]
+    inp = make_inputs(w, seed=1234 + list(WORKLOADS).index(name), device=dev)
+    row = {"workload": name, "note": w.note}
+    fused = measure(inp, steps, warmup, flush)
+    row["fused_cold_us"] = fused["cold_median_us"]
+    try:
+        call = unfused_call(inp)
+        ref = call()
+        got = fused_rope_attention(inp["q"], inp["k"], inp["v"], inp["cos"], inp["sin"], inp["cu_seqlens"],
+                                   inp["max_seqlen"])
+        torch.cuda.synchronize()
+        row["max_abs_diff"] = float((ref.float() - got.float()).abs().max())
+        m = time_calls(call, steps, warmup, flush)
+        row["unfused_cold_us"] = m["cold_median_us"]
+        row["speedup"] = m["cold_median_us"] / fused["cold_median_us"]
+    except Exception as e:  # an unsupported head_dim or backend: recorded, not fatal
+        row["unfused_error"] = f"{type(e).__name__}: {e}"[:300]
+    return row
+
+
 def run_backward(name: str, steps: int, warmup: int, flush: torch.Tensor, dev) -> dict:
     w = WORKLOADS[name]
     inp = make_inputs(w, seed=1234 + list(WORKLOADS).index(name), device=dev)
@@ -346,6 +393,9 @@ def main() -> int:
                          "device copy of --copy-mib MiB (HBM counter calibration), and exit")
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--bwd", action="store_true", help="profiling driver: run backward calls instead")
+    ap.add_argument("--comparator", default=None, metavar="FILE",
+                    help="time the unfused torch path (rotation + varlen_attn) beside the fused op for every "
+                         "workload and write them to FILE")
     ap.add_argument("--backward", default=None, metavar="FILE",
                     help="measure the backward of every workload and write them to FILE")
     ap.add_argument("--drift", default=None, metavar="FILE",
@@ -363,6 +413,17 @@ def main() -> int:
     flush = torch.ones(FLUSH_BYTES, dtype=torch.uint8, device=dev)
     if args.profile_calls:
         return profile_driver(args, flush, dev)
+    if args.comparator:
+        rows = []
+        for name in WORKLOADS:
+            r = run_comparator(name, max(10, args.steps // 2), max(3, args.warmup // 2), flush, dev)
+            rows.append(r)
+            print(f"[bench] comparator {name}: " + ", ".join(f"{k} {v:.4g}" if isinstance(v, float) else f"{k} {v}"
+                                                          for k, v in r.items() if k not in ("workload", "note")),
+                  file=sys.stderr, flush=True)
+        with open(args.comparator, "w") as f:
+            json.dump(rows, f, indent=1)
+        return 0
     if args.backward:
         rows = []
         for name in WORKLOADS:
