@@ -225,6 +225,35 @@ def unfused_call(inp):
     return call
 
 
+def train_step_calls(inp):
+    """Closures running forward + backward through autograd (dO ~ N(0, 1)):
+    the fused op, and the unfused path of ``unfused_call`` (whose rotation and
+    attention get their gradients from torch)."""
+    from torch.nn.attention.varlen import varlen_attn
+    q, k, v, cos, sin, cu = (inp[x] for x in ("q", "k", "v", "cos", "sin", "cu_seqlens"))
+    ms = inp["max_seqlen"]
+    half = q.shape[2] // 2
+    c, s = cos.float()[:, None, :], sin.float()[:, None, :]
+    g = torch.Generator(device=q.device).manual_seed(98)
+    dout = torch.randn(q.shape, generator=g, device=q.device).to(q.dtype)
+    qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+
+    def rot(x):
+        xf = x.float()
+        x0, x1 = xf[..., :half], xf[..., half:]
+        return torch.cat([x0 * c - x1 * s, x0 * s + x1 * c], -1).to(x.dtype)
+
+    def fused():
+        qg.grad = kg.grad = vg.grad = None
+        fused_rope_attention(qg, kg, vg, cos, sin, cu, ms).backward(dout)
+
+    def unfused():
+        qg.grad = kg.grad = vg.grad = None
+        varlen_attn(rot(qg), rot(kg), vg, cu, cu, ms, ms).backward(dout)
+
+    return fused, unfused
+
+
 def run_comparator(name: str, steps: int, warmup: int, flush: torch.Tensor, dev) -> dict:
     """The fused op and the unfused torch path on the same inputs and GPU:
     cold medians and their ratio (context only; the reference's published
@@ -244,6 +273,12 @@ def run_comparator(name: str, steps: int, warmup: int, flush: torch.Tensor, dev)
         m = time_calls(call, steps, warmup, flush)
         row["unfused_cold_us"] = m["cold_median_us"]
         row["speedup"] = m["cold_median_us"] / fused["cold_median_us"]
+        f_call, u_call = train_step_calls(inp)
+        mf = time_calls(f_call, steps, warmup, flush)
+        mu = time_calls(u_call, steps, warmup, flush)
+        row["fused_fwd_bwd_cold_us"] = mf["cold_median_us"]
+        row["unfused_fwd_bwd_cold_us"] = mu["cold_median_us"]
+        row["fwd_bwd_speedup"] = mu["cold_median_us"] / mf["cold_median_us"]
     except Exception as e:  # an unsupported head_dim or backend: recorded, not fatal
         row["unfused_error"] = f"{type(e).__name__}: {e}"[:300]
     return row
