@@ -819,6 +819,44 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         uint32_t col;      // this lane's byte offset in the row, kPadSlot for padding
         bool raw;          // raw part (K, cos, sin) or V
     };
+    // The bases and strides come in as parameters (values) on the generic
+    // path: there, selecting between captured variables would select between
+    // their addresses, which keeps them in scratch memory and puts every
+    // job's base behind a flat load in every iteration.  (The steady-state
+    // setup runs once; its descriptors stay as they are, which keeps the
+    // steady loop's registers as they are.)
+    auto job_desc_of = [&](int m, const char *kb_, const char *cb_, const char *sb_, const char *vb_, int64_t krs_,
+                           int64_t trs_, int64_t vrs_) {
+        const int gi = min(w + kLongWaves * m, NDMA - 1);
+        Job jb;
+        auto slot = [&](int ii, int pc, int dc) {  // pc, dc: compile-time in each branch
+            const int s = 64 * ii + lane, row = s / pc, c = s - row * pc;
+            jb.row = row;
+            jb.col = c < dc ? (uint32_t)(16 * c) : kPadSlot;
+        };
+        if (gi < KPC) {
+            jb.base = kb_;
+            jb.rows = (uint32_t)krs_;
+            jb.lds0 = (uint32_t)(gi * 1024);
+            slot(gi, KPC, KCH);
+        } else if (gi < NRAWI) {
+            const bool is_cos = gi < KPC + TPC;
+            const int ii = is_cos ? gi - KPC : gi - KPC - TPC;
+            jb.base = is_cos ? cb_ : sb_;
+            jb.rows = (uint32_t)trs_;
+            jb.lds0 = (uint32_t)(LDS::kRawK + (is_cos ? 0 : LDS::kRawT) + ii * 1024);
+            slot(ii, TPC, TCH);
+        } else {
+            const int ii = gi - NRAWI;
+            jb.base = vb_;
+            jb.rows = (uint32_t)vrs_;
+            jb.lds0 = (uint32_t)(LDS::kOffV + ii * 1024);
+            slot(ii, VPC, KCH);
+        }
+        jb.raw = gi < NRAWI;
+        jb.bufstep = jb.raw ? LDS::kRaw : LDS::kV;
+        return jb;
+    };
     auto job_desc = [&](int m) {
         const int gi = min(w + kLongWaves * m, NDMA - 1);
         Job jb;
@@ -857,7 +895,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     // Generic path: prologue and last iterations.
     auto job_generic = [&](int m, int xr, int br, int xv, int bv) {
         if (!has_job(m)) return;
-        const Job jb = job_desc(m);
+        const Job jb = job_desc_of(m, kbase, cbase, sbase, vbase, krs, trs, vrs);
         const int x = jb.raw ? xr : xv, bf = jb.raw ? br : bv;
         if (x >= nblk) return;
         const int nkv = min(kLongBKV, Lkv - kLongBKV * x);
