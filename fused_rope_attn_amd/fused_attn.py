@@ -428,7 +428,8 @@ def fused_rope_attention_bwd(dout, q, k, v, cos, sin, out, lse, cu_seqlens, max_
 class _FusedRopeAttention(torch.autograd.Function):
     """Autograd node of the op: the forward also writes the log-sum-exp, the
     backward runs ``fra_bwd_varlen``.  cos/sin and cu_seqlens get no
-    gradient."""
+    gradient; the backward is not itself differentiable (double backward
+    raises)."""
 
     @staticmethod
     def forward(ctx, q, k, v, cos, sin, cu, max_seqlen, scale):
@@ -440,6 +441,7 @@ class _FusedRopeAttention(torch.autograd.Function):
         return out
 
     @staticmethod
+    @torch.autograd.function.once_differentiable
     def backward(ctx, dout):
         q, k, v, cos, sin, out, lse, cu = ctx.saved_tensors
         dq = torch.zeros(q.shape, dtype=q.dtype, device=q.device)

@@ -206,3 +206,14 @@ def test_backward_bf16_tables_widened(device):
     b = gpu_fwd_bwd(cf)
     for x, y in zip(a[2:], b[2:]):
         assert torch.equal(x, y)
+
+
+def test_double_backward_raises(device):
+    """The backward is not itself differentiable: a second derivative raises
+    instead of silently being zero."""
+    c = on(make_case([64], 1, 80, seed=660), device)
+    q = c["q"].clone().requires_grad_(True)
+    out = fused_rope_attention(q, c["k"], c["v"], c["cos"], c["sin"], c["cu"], c["max_seqlen"])
+    (gq,) = torch.autograd.grad(out, q, c["dout"], create_graph=True)
+    with pytest.raises(RuntimeError):
+        gq.float().sum().backward()
