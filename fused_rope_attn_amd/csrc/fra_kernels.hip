@@ -4,15 +4,22 @@
 // (reference fused_attn.py:235-423):
 //
 //   window_kernel  every segment has <= 64 tokens (Qwen2.5-VL window layers).
-//                  One wavefront owns one (segment, head): it loads Q and K
-//                  rows straight into MFMA operand registers, rotates them in
-//                  fp32 there, stages V transposed in LDS, and does one
-//                  64x64 softmax -- no online rescaling is needed.
+//                  One workgroup per (segment, group of 2 or 4 heads), one
+//                  wavefront per head: Q, K and the cos/sin rows are loaded
+//                  as coalesced slab rows, rotated in fp32 through LDS into
+//                  MFMA operand registers, V goes from HBM straight to LDS,
+//                  and each wavefront does one 64x64 softmax -- no online
+//                  rescaling is needed.
 //   long_kernel    segments of any length (full-attention layers).  Split-Q
-//                  flash tiling: a 4-wave workgroup owns 128 query rows of one
-//                  (segment, head); K is rotated once per 64-row block while
-//                  it is staged in LDS, V is staged transposed, and each wave
-//                  runs an exp2 online softmax over its 32 rows.
+//                  flash tiling: an 8-wave workgroup owns 256 query rows of
+//                  one (segment, head); K, V and the cos/sin rows of each
+//                  64-key block are staged in LDS by direct loads, K is rotated
+//                  once per block there, and each wave runs an exp2 online
+//                  softmax over its 32 rows.  A partly filled last round of
+//                  workgroups is split along the key range and merged by
+//                  split_merge_kernel.
+//
+// Both can also write the softmax log-sum-exp for the backward (fra_bwd.hip).
 //
 // Matrix products use v_mfma_f32_32x32x16_{bf16,f16}.  Scores are computed
 // transposed (S^T = K_rot Q_rot^T) so that the 32x32 accumulator layout puts
