@@ -217,3 +217,38 @@ def test_double_backward_raises(device):
     (gq,) = torch.autograd.grad(out, q, c["dout"], create_graph=True)
     with pytest.raises(RuntimeError):
         gq.float().sum().backward()
+
+
+@pytest.mark.parametrize("d,tdt", [(64, torch.bfloat16), (96, torch.float16), (72, torch.float32)])
+def test_backward_long_table_dtypes(device, d, tdt):
+    """Long segments at more head dims, with 16-bit tables (widened for the
+    backward) and int64 cu_seqlens, against the oracle."""
+    case = make_case([190, 70], 2, d, seed=670 + d)
+    case["cos"], case["sin"] = case["cos"].to(tdt), case["sin"].to(tdt)
+    case["cu"] = case["cu"].to(torch.int64)
+    out, lse, dq, dk, dv = gpu_fwd_bwd(on(case, device))
+    q, k, v, do = (f32(case[x]) for x in ("q", "k", "v", "dout"))
+    cos, sin, cu = f32(case["cos"]), f32(case["sin"]), case["cu"].numpy()
+    check_lse(f32(lse), A.softmax_lse(q, k, cos, sin, cu), f"d={d}")
+    rq, rk, rv = A.fused_rope_attention_bwd(do, q, k, v, cos, sin, cu)
+    check_grad(f32(dq), rq, f"d={d} dq")
+    check_grad(f32(dk), rk, f"d={d} dk")
+    check_grad(f32(dv), rv, f"d={d} dv")
+
+
+def test_backward_noncontiguous_dout(device):
+    """A dout that is a strided view (copied to the kernels' layout) gives the
+    same gradients as its contiguous copy."""
+    c = on(make_case([64, 50, 200], 2, 80, seed=690), device)
+    wide = torch.zeros(c["dout"].shape[0], 2, c["dout"].shape[1], c["dout"].shape[2], dtype=c["dout"].dtype,
+                       device=device)
+    wide[:, 1] = c["dout"]
+    strided = wide[:, 1]
+    assert not strided.is_contiguous()
+    out, lse = fused_rope_attention_fwd(c["q"], c["k"], c["v"], c["cos"], c["sin"], c["cu"], c["max_seqlen"])
+    a = fused_rope_attention_bwd(strided, c["q"], c["k"], c["v"], c["cos"], c["sin"], out, lse, c["cu"], c["max_seqlen"])
+    b = fused_rope_attention_bwd(c["dout"], c["q"], c["k"], c["v"], c["cos"], c["sin"], out, lse, c["cu"],
+                                 c["max_seqlen"])
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
