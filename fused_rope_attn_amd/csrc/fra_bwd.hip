@@ -51,6 +51,7 @@ struct BParams {
     const int32_t *cu;
     char *dq, *dk, *dv;
     float *dvec;  // [num_heads, total]: rowsum(dout * out)
+    char *qr, *kr;  // longer segments: q_rot, k_rot ([total, num_heads, head_dim], storage dtype)
     int64_t sq_s, sq_h, sk_s, sk_h, sv_s, sv_h, so_s, so_h, sdo_s, sdo_h;
     int64_t sdq_s, sdq_h, sdk_s, sdk_h, sdv_s, sdv_h, sr_s;
     int32_t total, num_heads, num_seqs;
@@ -263,6 +264,32 @@ __global__ __launch_bounds__(256) void bwd_dot_kernel(const BParams p) {
     p.dvec[(int64_t)h * p.total + t] = acc;
 }
 
+// q_rot and k_rot into the workspace ([total, heads, head_dim], dense), once
+// per call: the dq and dk/dv units then stage plain rows instead of rotating
+// every block they load (each K block is loaded by every query block of its
+// segment and head, and each Q block by every key block).  One thread per
+// (token, head, quad i): quads i of both halves, the forward's rotation.
+template <int D, class E, bool FULL>
+__global__ __launch_bounds__(256) void bwd_rotate_kernel(const BParams p) {
+    constexpr int NQ = D / 8, HALF = D / 2;
+    const int64_t it = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (it >= (int64_t)p.total * p.num_heads * NQ) return;
+    const int64_t row = it / NQ;
+    const int i = (int)(it - row * NQ);
+    const int t = (int)(row / p.num_heads), h = (int)(row - (int64_t)t * p.num_heads);
+    const char *crow = p.cos + (int64_t)t * p.sr_s * 4, *srow = p.sin + (int64_t)t * p.sr_s * 4;
+    const int64_t dst = ((int64_t)t * p.num_heads + h) * D * 2;
+    u32x2 r0, r1;
+    load_rotate_quad<D, E, FRA_DTYPE_F32, FULL>(p.q + ((int64_t)t * p.sq_s + (int64_t)h * p.sq_h) * 2, crow, srow, i,
+                                                true, r0, r1);
+    *(u32x2 *)(p.qr + dst + 8 * i) = r0;
+    *(u32x2 *)(p.qr + dst + 2 * HALF + 8 * i) = r1;
+    load_rotate_quad<D, E, FRA_DTYPE_F32, FULL>(p.k + ((int64_t)t * p.sk_s + (int64_t)h * p.sk_h) * 2, crow, srow, i,
+                                                true, r0, r1);
+    *(u32x2 *)(p.kr + dst + 8 * i) = r0;
+    *(u32x2 *)(p.kr + dst + 2 * HALF + 8 * i) = r1;
+}
+
 // A operand of X^T B for a row-major LDS region X (pitch PITCH bytes) by
 // ds_read_b64_tr_b16, as in the forward's PV product: for k-step (a, h) of
 // 16 rows and d tile dt, lane (r, g) receives X[32a + 16h + {4g..4g+3,
@@ -321,13 +348,11 @@ __device__ __forceinline__ void bwd_dq_unit(const BParams &p, char *lds, int uni
     const int nq = min(BQ, L - q0);
 
     // Q_rot of the block -> LDS -> the B operands of S^T (one query per lane).
+    const int64_t rrs = (int64_t)p.num_heads * D * 2;  // row stride of q_rot / k_rot (bytes)
     {
-        RotBlock<D, E, FULL, BQ, NT, 1> qb;
-        const char *const xq[1] = {p.q + ((int64_t)(s0 + q0) * p.sq_s + (int64_t)head * p.sq_h) * 2};
-        const int64_t xs[1] = {p.sq_s * 2};
-        qb.load(p, xq, xs, s0 + q0, nq, tid);
-        char *const dst[1] = {lds};
-        qb.store(dst, PRD, nq, tid);
+        RowBlock<D, BQ, NT> qb;
+        qb.load(p.qr + ((int64_t)(s0 + q0) * p.num_heads + head) * D * 2, rrs, nq, tid);
+        qb.store(lds, PRD, tid);
     }
     __syncthreads();
     const int qi = 32 * w + r;
@@ -353,16 +378,14 @@ __device__ __forceinline__ void bwd_dq_unit(const BParams &p, char *lds, int uni
     const int nkb = (L + BKV - 1) / BKV;
     // Key blocks through registers, one block ahead: block kb + 1's loads are
     // in flight while block kb is computed.
-    RotBlock<D, E, FULL, BKV, NT, 1> kbk;
+    RowBlock<D, BKV, NT> kbk;
     RowBlock<D, BKV, NT> vbk;
     auto load_block = [&](int kb) {
         const int k0 = kb * BKV, nk = min(BKV, L - k0);
-        const char *const xk[1] = {p.k + ((int64_t)(s0 + k0) * p.sk_s + (int64_t)head * p.sk_h) * 2};
-        const int64_t xs[1] = {p.sk_s * 2};
         // an opaque thread id: the items' addresses are recomputed per block
         // instead of being kept live across the loop
         const int ft = fresh(tid);
-        kbk.load(p, xk, xs, s0 + k0, nk, ft);
+        kbk.load(p.kr + ((int64_t)(s0 + k0) * p.num_heads + head) * D * 2, rrs, nk, ft);
         vbk.load(p.v + ((int64_t)(s0 + k0) * p.sv_s + (int64_t)head * p.sv_h) * 2, p.sv_s * 2, nk, ft);
     };
     // Block kb goes to LDS stage kb & 1 at the start of iteration kb - 1, so
@@ -372,8 +395,7 @@ __device__ __forceinline__ void bwd_dq_unit(const BParams &p, char *lds, int uni
         const int nk = min(BKV, L - kb * BKV);
         const int ft = fresh(tid);
         char *const base = lds + (kb & 1) * LDS::kStage;
-        char *const dst[1] = {base + kKr};
-        kbk.store(dst, PTR, nk, ft);
+        kbk.store(base + kKr, PTR, ft);
         vbk.store(base + kV, PRD, ft);
     };
     load_block(0);
@@ -477,13 +499,11 @@ __device__ __forceinline__ void bwd_dkdv_unit(const BParams &p, char *lds, int u
     const int nk = min(BKV, L - k0);
 
     // K_rot and V of the block -> the B operands of S and dP (one key per lane).
+    const int64_t rrs = (int64_t)p.num_heads * D * 2;  // row stride of q_rot / k_rot (bytes)
     {
-        RotBlock<D, E, FULL, BKV, NT, 1> kbk;
-        const char *const xk[1] = {p.k + ((int64_t)(s0 + k0) * p.sk_s + (int64_t)head * p.sk_h) * 2};
-        const int64_t xs[1] = {p.sk_s * 2};
-        kbk.load(p, xk, xs, s0 + k0, nk, tid);
-        char *const dst[1] = {lds};
-        kbk.store(dst, PRD, nk, tid);
+        RowBlock<D, BKV, NT> kbk;
+        kbk.load(p.kr + ((int64_t)(s0 + k0) * p.num_heads + head) * D * 2, rrs, nk, tid);
+        kbk.store(lds, PRD, tid);
     }
     __syncthreads();
     const int ki = 32 * w + r;
@@ -507,21 +527,16 @@ __device__ __forceinline__ void bwd_dkdv_unit(const BParams &p, char *lds, int u
     const uint32_t trl = tr_lane_offset<PTR>(lane);
     const int nqb = (L + BQ - 1) / BQ;
     // Query blocks through registers, one block ahead: block qb + 1's loads
-    // are in flight while block qb is computed.  Full-width tables (twice the
-    // table registers) would spill that way: they load each block at the top
-    // of its own iteration.
-    constexpr bool AHEAD = !FULL;
-    RotBlock<D, E, FULL, BQ, NT, 1> qbk;
+    // are in flight while block qb is computed.
+    RowBlock<D, BQ, NT> qbk;
     RowBlock<D, BQ, NT> dbk;
     float lv, dvv;
     auto load_block = [&](int qb) {
         const int q0 = qb * BQ, nq = min(BQ, L - q0);
-        const char *const xq[1] = {p.q + ((int64_t)(s0 + q0) * p.sq_s + (int64_t)head * p.sq_h) * 2};
-        const int64_t xs[1] = {p.sq_s * 2};
         // an opaque thread id: the items' addresses are recomputed per block
         // instead of being kept live across the loop
         const int ft = fresh(tid);
-        qbk.load(p, xq, xs, s0 + q0, nq, ft);
+        qbk.load(p.qr + ((int64_t)(s0 + q0) * p.num_heads + head) * D * 2, rrs, nq, ft);
         dbk.load(p.dout + ((int64_t)(s0 + q0) * p.sdo_s + (int64_t)head * p.sdo_h) * 2, p.sdo_s * 2, nq, ft);
         // Rows past the segment: lse = +inf makes their P (and dZ) zero.
         lv = __builtin_inff();
@@ -539,8 +554,7 @@ __device__ __forceinline__ void bwd_dkdv_unit(const BParams &p, char *lds, int u
         const int nq = min(BQ, L - qb * BQ);
         const int ft = fresh(tid);
         char *const base = lds + (qb & 1) * LDS::kStage;
-        char *const dst[1] = {base + kQr};
-        qbk.store(dst, PTR, nq, ft);
+        qbk.store(base + kQr, PTR, ft);
         dbk.store(base + kDo, PTR, ft);
         if (ft < BQ) {
             ((float *)(base + kLse))[ft] = lv;
@@ -550,18 +564,13 @@ __device__ __forceinline__ void bwd_dkdv_unit(const BParams &p, char *lds, int u
     load_block(0);
     __syncthreads();  // K_rot's rows are in registers: stage 0 may go over them
     store_block(0);
-    if constexpr (AHEAD) {
-        if (nqb > 1) load_block(1);
-    }
+    if (nqb > 1) load_block(1);
     __syncthreads();
     for (int qb = 0; qb < nqb; ++qb) {
         const int q0 = qb * BQ, nq = min(BQ, L - q0);
         if (qb + 1 < nqb) {
-            if constexpr (!AHEAD) load_block(qb + 1);
             store_block(qb + 1);  // the other stage: its last reader (block qb - 1) passed the barrier
-            if constexpr (AHEAD) {
-                if (qb + 2 < nqb) load_block(qb + 2);
-            }
+            if (qb + 2 < nqb) load_block(qb + 2);
         }
         const char *const stage = lds + (qb & 1) * LDS::kStage;
         const float *lsef = (const float *)(stage + kLse);
@@ -906,15 +915,15 @@ void bwd_window_kernel(const BParams p) {
 typedef void (*BwdFn)(BParams);
 
 struct BwdKernels {
-    BwdFn dot, matrix;  // longer segments: Dvec, then dq and dk/dv units in one launch
+    BwdFn dot, rotate, matrix;  // longer segments: Dvec, q_rot / k_rot, then dq and dk/dv units
     int nw;
     BwdFn window;  // every segment <= 64 tokens: the one-pass kernel
 };
 
 template <int D, class E, bool FULL, int NW>
 BwdKernels bwd_kernels_nw() {
-    return BwdKernels{(BwdFn)bwd_dot_kernel<D, E>, (BwdFn)bwd_long_kernel<D, E, FULL, NW>, NW,
-                      (BwdFn)bwd_window_kernel<D, E, FULL>};
+    return BwdKernels{(BwdFn)bwd_dot_kernel<D, E>, (BwdFn)bwd_rotate_kernel<D, E, FULL>,
+                      (BwdFn)bwd_long_kernel<D, E, FULL, NW>, NW, (BwdFn)bwd_window_kernel<D, E, FULL>};
 }
 
 template <int D, class E>
@@ -940,9 +949,13 @@ bool bwd_pick(int d, int qkv, bool full, BwdKernels &k) {
 
 bool aligned_to(const void *ptr, int bytes) { return ((uintptr_t)ptr % (uintptr_t)bytes) == 0; }
 
-// Scratch of the two-kernel path (Dvec); the one-pass window kernel needs none.
+// Scratch of the longer-segment path: Dvec ([H, N] fp32, padded to 256
+// bytes), then q_rot and k_rot ([N, H, D] in the storage dtype).  The
+// one-pass window kernel needs none.
+int64_t bwd_ws_dvec_bytes(const fra_bwd_args *a) { return ((int64_t)a->num_heads * a->total_seq * 4 + 255) / 256 * 256; }
+int64_t bwd_ws_rot_bytes(const fra_bwd_args *a) { return (int64_t)a->total_seq * a->num_heads * a->head_dim * 2; }
 int64_t bwd_ws_bytes(const fra_bwd_args *a) {
-    return a->max_seqlen <= 64 ? 0 : (int64_t)a->num_heads * a->total_seq * 4;
+    return a->max_seqlen <= 64 ? 0 : bwd_ws_dvec_bytes(a) + 2 * bwd_ws_rot_bytes(a);
 }
 
 int bwd_check(const fra_bwd_args *a) {
@@ -1034,6 +1047,8 @@ int fra_bwd_varlen(const fra_bwd_args *a, void *stream) {
     p.dk = (char *)a->dk;
     p.dv = (char *)a->dv;
     p.dvec = (float *)a->workspace;
+    p.qr = (char *)a->workspace + bwd_ws_dvec_bytes(a);
+    p.kr = p.qr + bwd_ws_rot_bytes(a);
     p.sq_s = a->q_stride_seq;
     p.sq_h = a->q_stride_head;
     p.sk_s = a->k_stride_seq;
@@ -1075,9 +1090,14 @@ int fra_bwd_varlen(const fra_bwd_args *a, void *stream) {
     if (grid_dot > 0x7fffffff || grid > 0x7fffffff)
         return fra_fail(FRA_EUNSUPPORTED, "grid of %lld workgroups is too large", (long long)std::max(grid, grid_dot));
     p.blocks = (int32_t)blocks;
+    const int64_t grid_rot = (rows * (d / 8) + 255) / 256;
+    if (grid_rot > 0x7fffffff) return fra_fail(FRA_EUNSUPPORTED, "grid of %lld workgroups is too large", (long long)grid_rot);
     hipLaunchKernelGGL(k.dot, dim3((unsigned)grid_dot), dim3(256), 0, st, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fra_fail(FRA_EHIP, "launch of the backward row dot products failed: %s", hipGetErrorString(e));
+    hipLaunchKernelGGL(k.rotate, dim3((unsigned)grid_rot), dim3(256), 0, st, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fra_fail(FRA_EHIP, "launch of the backward rotation failed: %s", hipGetErrorString(e));
     hipLaunchKernelGGL(k.matrix, dim3((unsigned)grid), dim3(64 * k.nw), 0, st, p);
     e = hipGetLastError();
     if (e != hipSuccess) return fra_fail(FRA_EHIP, "launch of the dq / dk,dv kernel failed: %s", hipGetErrorString(e));

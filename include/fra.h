@@ -199,8 +199,9 @@ typedef struct fra_bwd_args {
     int32_t rope_dtype;
     float softmax_scale;
     int32_t flags;              /* reserved, must be 0 */
-    /* Required device scratch of at least fra_bwd_workspace_bytes() bytes
-     * (the per-row dot products of dout and out); 16-byte aligned. */
+    /* Device scratch of at least fra_bwd_workspace_bytes() bytes, 16-byte
+     * aligned: the per-row dot products of dout and out, and q and k rotated
+     * once per call.  None (0 bytes) when max_seqlen <= 64. */
     void *workspace;
     int64_t workspace_bytes;
 } fra_bwd_args;

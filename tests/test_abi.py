@@ -173,7 +173,9 @@ def test_bwd_struct_and_workspace_size():
     nbytes = ctypes.c_int64(-1)
     a = make_bwd_args(n=9216, h=16, max_seqlen=9216, nseg=1)
     assert lib.fra_bwd_workspace_bytes(a, ctypes.byref(nbytes)) == _lib.FRA_OK
-    assert nbytes.value == 9216 * 16 * 4  # one fp32 per (head, token): the rows' dout . out
+    # one fp32 per (head, token) for the rows' dout . out (256-byte padded),
+    # then q and k rotated once ([N, H, D], 2 bytes each)
+    assert nbytes.value == (9216 * 16 * 4 + 255) // 256 * 256 + 2 * 9216 * 16 * 80 * 2
     # segments of at most 64 tokens take the one-pass kernel, which needs no scratch
     assert lib.fra_bwd_workspace_bytes(make_bwd_args(n=9216, nseg=144), ctypes.byref(nbytes)) == _lib.FRA_OK
     assert nbytes.value == 0
@@ -208,5 +210,5 @@ def test_bwd_requires_workspace():
     a = make_bwd_args(max_seqlen=1000, nseg=1)
     assert lib.fra_bwd_varlen(a, None) == _lib.FRA_EINVAL  # no workspace: fails before any launch
     assert "workspace" in lib.fra_last_error().decode()
-    a.workspace, a.workspace_bytes = (1 << 20) * 20, 1024 * 16 * 4 - 4
+    a.workspace, a.workspace_bytes = (1 << 20) * 20, 1024 * 16 * 4 + 2 * 1024 * 16 * 80 * 2 - 4
     assert lib.fra_bwd_varlen(a, None) == _lib.FRA_EINVAL
