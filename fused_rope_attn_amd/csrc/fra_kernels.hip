@@ -62,6 +62,7 @@ struct KParams {
     int32_t dense_heads;  // window kernel: q, k, v and out have head stride == head_dim
     float scale_log2;     // softmax_scale * log2(e)
     float *lse;           // optional [num_heads, total] natural-log row sums (NULL: not written)
+    char *krot;           // long kernel, PRE variant: k_rot rows [total, num_heads, head_dim] (workspace)
 };
 
 // ---- window kernel ------------------------------------------------------------
@@ -596,7 +597,10 @@ constexpr int long_vpitch(int need) {
     return c;
 }
 
-template <int D, int RD, bool FULL> struct LongLds {
+// PRE: K comes rotated (k_rot rows in the caller's workspace, written by
+// krot_kernel once per call); the direct loads then fill the K_rot buffers
+// themselves and there is no raw staging or rotation in the loop.
+template <int D, int RD, bool FULL, bool PRE = false> struct LongLds {
     static constexpr int RB = RD == FRA_DTYPE_F32 ? 4 : 2;
     static constexpr int HALF = D / 2;
     static constexpr int W = FULL ? D : D / 2;         // table width
@@ -620,13 +624,37 @@ template <int D, int RD, bool FULL> struct LongLds {
     static constexpr int kRaw = kRawK + 2 * kRawT;     // raw K, cos, sin of one block
     static constexpr int kKrot = kLongBKV * KS * 2;
     static constexpr int kV = 64 * VPC * 16;
-    static constexpr int kRawBufs = 2 * (kRaw + kKrot + kV) <= kLdsLimit ? 2 : 1;
-    static constexpr int kOffKrot = kRawBufs * kRaw;
+    static constexpr int KRC = KS * 2 / 16;            // K_rot row pitch in 16-byte chunks (odd)
+    static constexpr int kRawBufs = PRE ? 2 : (2 * (kRaw + kKrot + kV) <= kLdsLimit ? 2 : 1);
+    static constexpr int kOffKrot = PRE ? 0 : kRawBufs * kRaw;
     static constexpr int kOffV = kOffKrot + 2 * kKrot;
     static constexpr int kBytes = kOffV + 2 * kV;
     static_assert(kBytes <= kLdsLimit, "long kernel LDS budget");
     static_assert(W * RB % 16 == 0, "table rows must be whole 16-byte chunks");
 };
+
+// k_rot = rot(k) for every row, [total, heads, head_dim] dense, into the
+// workspace: the long kernel's PRE variant then stages K_rot blocks
+// directly instead of staging raw K and the tables and rotating each block
+// once per query block (reference fused_attn.py:364-390 recomputes it per
+// query block too).  One thread per (token, head, quad i): quads i of both
+// halves, rotate_quad's arithmetic.
+template <int D, class E, int RD, bool FULL>
+__global__ __launch_bounds__(256) void krot_kernel(const KParams p) {
+    constexpr int NQ = D / 8, HALF = D / 2, RB = Rope<RD>::kBytes;
+    const int64_t it = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (it >= (int64_t)p.total * p.num_heads * NQ) return;
+    const int64_t row = it / NQ;
+    const int i = (int)(it - row * NQ);
+    const int t = (int)(row / p.num_heads), h = (int)(row - (int64_t)t * p.num_heads);
+    u32x2 r0, r1;
+    load_rotate_quad<D, E, RD, FULL>(p.k + ((int64_t)t * p.sk_s + (int64_t)h * p.sk_h) * 2,
+                                     p.cos + (int64_t)t * p.sr_s * RB, p.sin + (int64_t)t * p.sr_s * RB, i, true,
+                                     r0, r1);
+    char *dst = p.krot + row * (D * 2);
+    *(u32x2 *)(dst + 8 * i) = r0;
+    *(u32x2 *)(dst + 2 * HALF + 8 * i) = r1;
+}
 
 // ---- split last round: partial results and their merge ------------------------
 //
@@ -635,6 +663,7 @@ template <int D, int RD, bool FULL> struct LongLds {
 // l (row sum of P).  split_merge_kernel, launched after the long kernel on
 // the same stream, merges the parts of each unit into the output.
 constexpr int kSplitMaxParts = 8;
+constexpr int kSplitMinBlocks = 8;  // key blocks per part, at least
 
 __host__ __device__ constexpr int split_row_floats(int d) { return (d + 2 + 3) / 4 * 4; }  // 16-byte pitch
 
@@ -725,9 +754,9 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const KParams p) {
     *(u32x2 *)(orow + 8 * c) = u32x2{E::pack(acc[0] * inv, acc[1] * inv), E::pack(acc[2] * inv, acc[3] * inv)};
 }
 
-template <int D, class E, int RD, bool FULL>
+template <int D, class E, int RD, bool FULL, bool PRE>
 __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) {
-    using LDS = LongLds<D, RD, FULL>;
+    using LDS = LongLds<D, RD, FULL, PRE>;
     constexpr int HALF = D / 2;
     constexpr int NQ = D / 8;                  // quads per half
     constexpr int DP = LDS::DP;
@@ -737,13 +766,17 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     constexpr int RB = LDS::RB;
     constexpr int KCH = LDS::KCH, TCH = LDS::TCH;
     constexpr int KPC = LDS::KPC, TPC = LDS::TPC, VPC = LDS::VPC;
-    constexpr int NRAWI = KPC + 2 * TPC;       // direct loads of one raw block
+    constexpr int KRC = LDS::KRC;
+    static_assert(KRC % 2 == 1 && KRC * 16 == LDS::KS * 2, "K_rot rows are whole, odd numbers of chunks");
+    constexpr int NRAWI = PRE ? KRC : KPC + 2 * TPC;  // direct loads of one raw block (PRE: K_rot rows)
     constexpr int NDMA = NRAWI + VPC;          // ... plus the V block
     constexpr int MPER = (NDMA + kLongWaves - 1) / kLongWaves;
     constexpr int RPER = (NQ + kLongWaves - 1) / kLongWaves;  // rotation quads per wavefront
     constexpr bool ONES = LDS::kOnesCol;
     constexpr int RAWBUFS = LDS::kRawBufs;
-    constexpr int DIST = RAWBUFS + 1;          // raw K of block j + DIST is loaded in iteration j
+    // raw K of block j + DIST is loaded in iteration j (PRE: K_rot of block
+    // j + 2, into the K_rot buffer the rotation would otherwise fill then)
+    constexpr int DIST = PRE ? 2 : RAWBUFS + 1;
     typedef short v4i16 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
     typedef __attribute__((address_space(3))) void lds_void;
@@ -780,11 +813,12 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     const int nblk = (Lkv + kLongBKV - 1) / kLongBKV;
 
     const int64_t k0 = (int64_t)s0 + (int64_t)kLongBKV * b0;  // first key row
-    const char *kbase = p.k + (k0 * p.sk_s + (int64_t)head * p.sk_h) * 2;
+    const char *kbase = PRE ? p.krot + (k0 * p.num_heads + head) * (int64_t)(D * 2)
+                            : p.k + (k0 * p.sk_s + (int64_t)head * p.sk_h) * 2;
     const char *vbase = p.v + (k0 * p.sv_s + (int64_t)head * p.sv_h) * 2;
     const char *cbase = p.cos + k0 * p.sr_s * RB;
     const char *sbase = p.sin + k0 * p.sr_s * RB;
-    const int64_t krs = p.sk_s * 2, vrs = p.sv_s * 2, trs = p.sr_s * RB;
+    const int64_t krs = PRE ? (int64_t)p.num_heads * D * 2 : p.sk_s * 2, vrs = p.sv_s * 2, trs = p.sr_s * RB;
 
     const float sl = p.scale_log2;
     float m_i = kNegInf, l_i = 0.f;  // running max (scale*log2e units) and row sum
@@ -841,27 +875,42 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
             jb.row = row;
             jb.col = c < dc ? (uint32_t)(16 * c) : kPadSlot;
         };
-        if (gi < KPC) {
-            jb.base = kb_;
-            jb.rows = (uint32_t)krs_;
+        // Base and row stride as selects of values (unary + makes each
+        // operand a prvalue), outside the branches: a branch per source that
+        // loads its own variable is merged into a load through a select of
+        // their addresses, which keeps them in scratch memory.
+        const bool is_k = PRE ? gi < NRAWI : gi < KPC;
+        const bool is_t = !PRE && !is_k && gi < NRAWI;
+        const bool is_c = gi < KPC + TPC;
+        if constexpr (PRE) {
+            // Two sources: the loaded values pass through empty asm first,
+            // or the select is folded back into a load through a select of
+            // the captured variables' addresses.
+            uint64_t kv = (uint64_t)kb_, vv = (uint64_t)vb_;
+            asm volatile("" : "+s"(kv), "+s"(vv));
+            jb.base = (const char *)(is_k ? kv : vv);
+            jb.rows = (uint32_t)(is_k ? +krs_ : +vrs_);
+        } else {
+            jb.base = is_k ? +kb_ : is_t ? (is_c ? +cb_ : +sb_) : +vb_;
+            jb.rows = (uint32_t)(is_k ? +krs_ : is_t ? +trs_ : +vrs_);
+        }
+        if (PRE && gi < NRAWI) {
+            jb.lds0 = (uint32_t)(LDS::kOffKrot + gi * 1024);
+            slot(gi, KRC, KCH);
+        } else if (!PRE && gi < KPC) {
             jb.lds0 = (uint32_t)(gi * 1024);
             slot(gi, KPC, KCH);
-        } else if (gi < NRAWI) {
-            const bool is_cos = gi < KPC + TPC;
-            const int ii = is_cos ? gi - KPC : gi - KPC - TPC;
-            jb.base = is_cos ? cb_ : sb_;
-            jb.rows = (uint32_t)trs_;
-            jb.lds0 = (uint32_t)(LDS::kRawK + (is_cos ? 0 : LDS::kRawT) + ii * 1024);
+        } else if (!PRE && gi < NRAWI) {
+            const int ii = is_c ? gi - KPC : gi - KPC - TPC;
+            jb.lds0 = (uint32_t)(LDS::kRawK + (is_c ? 0 : LDS::kRawT) + ii * 1024);
             slot(ii, TPC, TCH);
         } else {
             const int ii = gi - NRAWI;
-            jb.base = vb_;
-            jb.rows = (uint32_t)vrs_;
             jb.lds0 = (uint32_t)(LDS::kOffV + ii * 1024);
             slot(ii, VPC, KCH);
         }
         jb.raw = gi < NRAWI;
-        jb.bufstep = jb.raw ? LDS::kRaw : LDS::kV;
+        jb.bufstep = jb.raw ? (PRE ? LDS::kKrot : LDS::kRaw) : LDS::kV;
         return jb;
     };
     auto job_desc = [&](int m) {
@@ -872,12 +921,17 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
             jb.row = row;
             jb.col = c < dc ? (uint32_t)(16 * c) : kPadSlot;
         };
-        if (gi < KPC) {
+        if (PRE && gi < NRAWI) {
+            jb.base = kbase;
+            jb.rows = (uint32_t)krs;
+            jb.lds0 = (uint32_t)(LDS::kOffKrot + gi * 1024);
+            slot(gi, KRC, KCH);
+        } else if (!PRE && gi < KPC) {
             jb.base = kbase;
             jb.rows = (uint32_t)krs;
             jb.lds0 = (uint32_t)(gi * 1024);
             slot(gi, KPC, KCH);
-        } else if (gi < NRAWI) {
+        } else if (!PRE && gi < NRAWI) {
             const bool is_cos = gi < KPC + TPC;
             const int ii = is_cos ? gi - KPC : gi - KPC - TPC;
             jb.base = is_cos ? cbase : sbase;
@@ -892,7 +946,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
             slot(ii, VPC, KCH);
         }
         jb.raw = gi < NRAWI;
-        jb.bufstep = jb.raw ? LDS::kRaw : LDS::kV;
+        jb.bufstep = jb.raw ? (PRE ? LDS::kKrot : LDS::kRaw) : LDS::kV;
         return jb;
     };
     // Does this wavefront have job m?
@@ -1007,20 +1061,25 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     }
     wait_dma();
     __syncthreads();
-    rotate(0, 0);
-    if constexpr (RAWBUFS == 2) {
-        if (nblk > 1) rotate(1, 1);
-        __syncthreads();
-#pragma unroll
-        for (int m = 0; m < MPER; ++m) job_generic(m, 2, 0, nblk, 0);  // raw K(2)
+    if constexpr (PRE) {
+        // K_rot(0), K_rot(1) and V(0) are in place; K_rot(2) goes to buffer 0
+        // in iteration 0, after the first S^T below has read K_rot(0).
     } else {
-        __syncthreads();
+        rotate(0, 0);
+        if constexpr (RAWBUFS == 2) {
+            if (nblk > 1) rotate(1, 1);
+            __syncthreads();
 #pragma unroll
-        for (int m = 0; m < MPER; ++m) job_generic(m, 1, 0, nblk, 0);  // raw K(1)
-        wait_dma();
-        __syncthreads();
-        if (nblk > 1) rotate(0, 1);
-        __syncthreads();
+            for (int m = 0; m < MPER; ++m) job_generic(m, 2, 0, nblk, 0);  // raw K(2)
+        } else {
+            __syncthreads();
+#pragma unroll
+            for (int m = 0; m < MPER; ++m) job_generic(m, 1, 0, nblk, 0);  // raw K(1)
+            wait_dma();
+            __syncthreads();
+            if (nblk > 1) rotate(0, 1);
+            __syncthreads();
+        }
     }
 
     // Per-lane LDS byte offsets.  K_rot A operand of S^T: row 32a + r, elements
@@ -1187,11 +1246,13 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
             __syncthreads();
         }
         pv(j, pop);
-        if (kLongWaves <= NQ || w < NQ) rotate_one(RB2, P, w);
+        if constexpr (!PRE) {
+            if (kLongWaves <= NQ || w < NQ) rotate_one(RB2, P, w);
+        }
         if constexpr (RAWBUFS == 2 && MPER > MFULL) {
             if (has_job(MFULL)) job_steady(MFULL, P);
         }
-        rotate_rest(RB2, P);
+        if constexpr (!PRE) rotate_rest(RB2, P);
         wait_dma();
         __syncthreads();
     };
@@ -1206,7 +1267,9 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
             __syncthreads();
         }
         pv(j, pop);
-        if (j + 2 < nblk) rotate((j + 2) % RAWBUFS, j & 1);
+        if constexpr (!PRE) {
+            if (j + 2 < nblk) rotate((j + 2) % RAWBUFS, j & 1);
+        }
         wait_dma();
         __syncthreads();
     };
@@ -1219,7 +1282,9 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     if (nblk - DIST - 1 >= 2) {
 #pragma unroll
         for (int m = 0; m < MPER; ++m) {
-            const Job jb = job_desc(m);
+            Job jb;
+            if constexpr (PRE) jb = job_desc_of(m, kbase, cbase, sbase, vbase, krs, trs, vrs);
+            else jb = job_desc(m);
             jstep[m] = kLongBKV * jb.rows;
             jptr[m] = jb.base + (int64_t)(jb.raw ? DIST : 1) * jstep[m];
             jvoff[m] = jb.col == kPadSlot ? kPadSlot : (uint32_t)jb.row * jb.rows + jb.col;
@@ -1292,7 +1357,11 @@ constexpr int kWindowMaxD = 96;
 
 struct Choice {
     KernelFn fn;
-    KernelFn merge;  // split_merge_kernel of the long kernel's instance
+    KernelFn merge;   // split_merge_kernel of the long kernel's instance
+    KernelFn fn_pre;  // long kernel, PRE variant (K rotated beforehand by krot)
+    KernelFn krot;    // krot_kernel of the instance
+    int lds_pre;
+    int pre;          // the plan uses fn_pre and krot
     int kernel, grid, block, block_q, block_kv, lds, split_units, split_parts;
     int heads;       // window kernel: heads (wavefronts) per workgroup
     int per_cu;      // window kernel: workgroups resident per CU
@@ -1322,7 +1391,10 @@ int device_cus() {
 // The long kernel's split last round.  Units (segment, head, query block)
 // run one workgroup per CU; when the last round of workgroups leaves CUs
 // idle, its units are split into up to kSplitMaxParts parts of their key
-// range (at least two key blocks each on the longest segment).  Each part
+// range, at least kSplitMinBlocks key blocks each on the longest segment
+// (shorter parts lose more to the partial writes and the merge launch than
+// the shorter last round gains: measured 8 us slower at 4 and 8 key
+// blocks per segment, 16 x 80 heads).  Each part
 // writes its unnormalised rows, running max and row sum to the workspace;
 // split_merge_kernel, the next launch on the stream, combines them.
 struct SplitPlan {
@@ -1337,7 +1409,7 @@ SplitPlan split_plan(int64_t units, int max_seqlen, int d) {
     const int64_t rounds = (units + slots - 1) / slots;
     const int64_t tail = units - (rounds - 1) * slots;
     int parts = (int)std::min<int64_t>(slots / tail, kSplitMaxParts);
-    parts = std::min(parts, ((max_seqlen + kLongBKV - 1) / kLongBKV) / 2);
+    parts = std::min(parts, ((max_seqlen + kLongBKV - 1) / kLongBKV) / kSplitMinBlocks);
     if (parts < 2) return sp;
     sp.units = tail;
     sp.parts = parts;
@@ -1369,9 +1441,12 @@ template <int D, class E, int RD, bool FULL> void pick_full(bool window, int hw,
         }
     }
     if constexpr (long_ok<D, RD, FULL>()) {
-        c.fn = (KernelFn)long_kernel<D, E, RD, FULL>;
+        c.fn = (KernelFn)long_kernel<D, E, RD, FULL, false>;
         c.merge = (KernelFn)split_merge_kernel<D, E>;
         c.lds = LongLds<D, RD, FULL>::kBytes;
+        c.fn_pre = (KernelFn)long_kernel<D, E, RD, FULL, true>;
+        c.krot = (KernelFn)krot_kernel<D, E, RD, FULL>;
+        c.lds_pre = LongLds<D, RD, FULL, true>::kBytes;
     }
 }
 
@@ -1407,6 +1482,12 @@ bool pick_kernel(int d, bool window, int hw, bool full, int qkv, int rd, Choice 
 }
 
 bool aligned(const void *ptr, int bytes) { return ((uintptr_t)ptr % (uintptr_t)bytes) == 0; }
+
+// Bytes of the k_rot rows the long kernel's PRE variant reads (rounded up to
+// 256 so the split scratch after them stays aligned).
+int64_t krot_workspace_bytes(const fra_fwd_args *a) {
+    return ((int64_t)a->total_seq * a->num_heads * a->head_dim * 2 + 255) / 256 * 256;
+}
 
 const char *dtype_name(int dt) {
     switch (dt) {
@@ -1506,7 +1587,9 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
     kp.max_seqlen = a->max_seqlen;
     kp.scale_log2 = a->softmax_scale * kLog2e;
     kp.lse = a->lse;
+    kp.krot = nullptr;
     if (a->lse && !aligned(a->lse, 4)) return fail(FRA_EINVAL, "lse must be 4-byte aligned");
+    if (a->workspace && !aligned(a->workspace, 16)) return fail(FRA_EINVAL, "workspace must be 16-byte aligned");
 
     const int64_t sh = (int64_t)a->num_seqs * a->num_heads;
     int64_t grid;
@@ -1539,9 +1622,24 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
         const SplitPlan sp = split_plan(units, a->max_seqlen, d);
         kp.tail_first = (int32_t)std::min<int64_t>(units, 0x7fffffff);
         kp.tail_split = 1;
+        // Workspace: [k_rot rows | split scratch].  With room for k_rot the
+        // PRE variant runs (krot_kernel first); the rest, if enough, holds
+        // the split scratch.  Without it (e.g. sized for the split alone)
+        // the kernel stages raw K and rotates it per block.
+        const int64_t kr_bytes = krot_workspace_bytes(a);
+        int64_t ws_left = a->workspace_bytes;
         kp.ws = (char *)a->workspace;
+        c.pre = 0;
+        if (a->workspace && a->workspace_bytes >= kr_bytes && c.fn_pre) {
+            c.pre = 1;
+            c.fn = c.fn_pre;
+            c.lds = c.lds_pre;
+            kp.krot = (char *)a->workspace;
+            kp.ws = (char *)a->workspace + kr_bytes;
+            ws_left -= kr_bytes;
+        }
         grid = units;
-        if (sp.parts > 1 && a->workspace_bytes >= sp.bytes) {
+        if (sp.parts > 1 && ws_left >= sp.bytes) {
             kp.tail_first = (int32_t)(units - sp.units);
             kp.tail_split = sp.parts;
             grid = kp.tail_first + sp.units * sp.parts;
@@ -1581,6 +1679,14 @@ int fra_fwd_varlen(const fra_fwd_args *args, void *stream) {
     if (args->total_seq == 0) return FRA_OK;
     if (c.split_parts > 1 && !args->workspace)
         return fail(FRA_EINVAL, "workspace_bytes is set but workspace is NULL");
+    if (c.pre) {
+        const int64_t items = (int64_t)args->total_seq * args->num_heads * (args->head_dim / 8);
+        const int64_t blocks = (items + 255) / 256;
+        if (blocks > 0x7fffffff) return fail(FRA_EUNSUPPORTED, "grid of %lld workgroups is too large", (long long)blocks);
+        hipLaunchKernelGGL(c.krot, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, kp);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fail(FRA_EHIP, "launch of the K rotation of %s failed: %s", c.name, hipGetErrorString(e));
+    }
     hipLaunchKernelGGL(c.fn, dim3(c.grid), dim3(c.block), 0, (hipStream_t)stream, kp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(FRA_EHIP, "launch of %s failed: %s", c.name, hipGetErrorString(e));
@@ -1605,7 +1711,7 @@ int fra_workspace_bytes(const fra_fwd_args *args, int64_t *bytes) {
     if (rc != FRA_OK) return rc;
     if (c.kernel == FRA_KERNEL_LONG) {
         const SplitPlan sp = split_plan((int64_t)a.num_seqs * a.num_heads * kp.qblocks, a.max_seqlen, a.head_dim);
-        if (sp.parts > 1) *bytes = sp.bytes;
+        *bytes = krot_workspace_bytes(&a) + (sp.parts > 1 ? sp.bytes : 0);
     }
     g_err[0] = 0;
     return FRA_OK;

@@ -88,14 +88,18 @@ typedef struct fra_fwd_args {
     float softmax_scale;        /* > 0; the reference uses 1/sqrt(head_dim) */
     int32_t flags;              /* reserved, must be 0 */
     /*
-     * Optional device workspace of the long kernel (no counterpart in the
-     * reference, whose launch takes no scratch memory).  When it holds at
-     * least the bytes fra_workspace_bytes() reports, the units of a partly
-     * filled last round of workgroups are split along the key range and a
-     * second, small kernel on the same stream merges their parts; otherwise
-     * (NULL / 0) nothing is split.  Scratch only: no contents are expected
-     * before the call or kept after it; calls that share a workspace must
-     * not overlap.
+     * Optional device workspace of the long kernel, 16-byte aligned (no
+     * counterpart in the reference, whose launch takes no scratch memory).
+     * Its first total_seq*num_heads*head_dim*2 bytes (rounded up to 256)
+     * take K rotated once per call by a small kernel launched first on the
+     * same stream, which the attention kernel then stages instead of
+     * rotating every key block once per query block.  When the whole holds
+     * what fra_workspace_bytes() reports, the rest also lets the units of a
+     * partly filled last round of workgroups split along the key range,
+     * with a second small kernel merging their parts.  Less than the rotated-K
+     * part (NULL / 0 included): K is rotated in the kernel and nothing is
+     * split.  Scratch only: no contents are expected before the call or
+     * kept after it; calls that share a workspace must not overlap.
      */
     void *workspace;
     int64_t workspace_bytes;
@@ -150,7 +154,8 @@ int fra_query_plan(const fra_fwd_args *args, fra_plan *plan);
 
 /*
  * Workspace bytes the long kernel can use for these arguments (their
- * workspace fields are ignored); 0 when no split applies.  No counterpart in
+ * workspace fields are ignored): rotated K plus the split scratch when a
+ * split applies; 0 for the window kernel.  No counterpart in
  * the reference (its Triton launch allocates nothing); callers that cannot
  * allocate simply pass no workspace and get the unsplit kernel.
  */

@@ -143,6 +143,27 @@ def test_forward_lse_pointer_alignment():
     assert "lse" in lib.fra_last_error().decode()
 
 
+def test_forward_workspace_size_and_alignment():
+    lib = _lib.load()
+    nbytes = ctypes.c_int64(-1)
+    assert lib.fra_workspace_bytes(make_args(), ctypes.byref(nbytes)) == _lib.FRA_OK
+    assert nbytes.value == 0  # window kernel: no workspace
+    n, h, d = 9216, 16, 80
+    a = make_args(n=n, nseg=1, max_seqlen=n, num_seqs=1)
+    assert lib.fra_workspace_bytes(a, ctypes.byref(nbytes)) == _lib.FRA_OK
+    krot = (n * h * d * 2 + 255) // 256 * 256  # K rotated once per call, then the split scratch
+    assert nbytes.value > krot
+    a.workspace, a.workspace_bytes = (1 << 20) * 10, nbytes.value
+    rc, p = plan_of(a)
+    assert rc == _lib.FRA_OK and p.split_parts > 1
+    a.workspace_bytes = krot  # rotated K only: no split
+    rc, p = plan_of(a)
+    assert rc == _lib.FRA_OK and p.split_parts == 0 and p.grid == h * ((n + p.block_q - 1) // p.block_q)
+    a.workspace = (1 << 20) * 10 + 8
+    assert lib.fra_fwd_varlen(a, None) == _lib.FRA_EINVAL
+    assert "workspace" in lib.fra_last_error().decode()
+
+
 def make_bwd_args(**kw):
     a = _lib.BwdArgs()
     n, h, d = kw.get("n", 1024), kw.get("h", 16), kw.get("d", 80)

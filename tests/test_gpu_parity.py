@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from fused_rope_attn_amd import fused_rope_attention, plan
+from fused_rope_attn_amd import _lib, fused_rope_attention, plan
 from fused_rope_attn_amd.configs import WORKLOADS, make_inputs
 from oracle import attention as A
 
@@ -317,12 +317,12 @@ def test_workload_parity(device, name):
         assert torch.equal(out_p, want)
 
 
-def _call_abi(case, device, workspace: bool):
-    """fra_fwd_varlen through the C ABI, with or without the long kernel's
-    workspace (without it, no unit is split)."""
+def _call_abi(case, device, workspace):
+    """fra_fwd_varlen through the C ABI, with the long kernel's whole
+    workspace (True), none (False: K rotated in the kernel, no unit split),
+    or "krot": only the rotated-K part (no split)."""
     import ctypes
 
-    from fused_rope_attn_amd import _lib
     from fused_rope_attn_amd.fused_attn import _build_args, _workspace_bytes
     args_t = {x: case[x].to(device) for x in ("q", "k", "v", "cos", "sin")}
     cu = case["cu_seqlens"].to(device=device, dtype=torch.int32)
@@ -332,6 +332,8 @@ def _call_abi(case, device, workspace: bool):
     lib = _lib.load()
     ws = None
     nbytes = _workspace_bytes(lib, a)
+    if workspace == "krot":
+        nbytes = (a.total_seq * a.num_heads * a.head_dim * 2 + 255) // 256 * 256
     if workspace and nbytes:
         ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=device)  # scratch: any contents
         a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
@@ -356,6 +358,24 @@ def test_long_kernel_split_last_round(device, lens, h, d):
     ref = oracle(case, heads=heads)
     got = f32(split if heads is None else split[:, heads])
     assert_close(got, ref, MAX_ABS, MEAN_ABS, f"split {lens}")
+
+
+@pytest.mark.parametrize("lens,h,d,rope_dtype,full", [
+    ([300, 5], 4, 80, torch.float32, False),
+    ([700, 1500, 64, 1], 2, 72, torch.float32, True),
+    ([520, 130], 3, 64, torch.bfloat16, False),
+    ([333], 2, 128, torch.float16, True),
+])
+def test_long_kernel_rotated_k_workspace(device, lens, h, d, rope_dtype, full):
+    # K rotated once per call into the workspace (a separate kernel) and then
+    # staged, against K rotated per block inside the kernel: both round the
+    # same fp32 rotation to the storage dtype, so the outputs are identical
+    case = random_case(lens, h=h, d=d, seed=270 + d, rope_dtype=rope_dtype, width=d if full else d // 2)
+    pre, pl = _call_abi(case, device, workspace="krot")
+    inkernel, pl0 = _call_abi(case, device, workspace=False)
+    assert pl.kernel == _lib.FRA_KERNEL_LONG and pl.split_parts == 0 and pl0.split_parts == 0
+    assert torch.equal(pre, inkernel), f"rotated-K workspace vs in-kernel rotation {lens}"
+    assert_close(f32(pre), oracle(case), MAX_ABS, MEAN_ABS, f"rotated-K workspace {lens}")
 
 
 # ---- known answers (tests/golden/attention_kat.npz, float64 from the definition) ----
