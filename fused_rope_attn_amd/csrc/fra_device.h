@@ -108,6 +108,20 @@ __device__ __forceinline__ void permlane32_swap(float &a, float &b) {
     asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
 
+// One direct load per lane: 16 bytes from src to LDS byte address
+// lds_addr + 16 * lane (lds_addr wave-uniform).  The compiler counts a
+// direct load as an LDS store of unknown place, and then makes every later
+// transposed LDS read wait (vmcnt(0)) for every direct load in flight,
+// whichever buffer either touches; issued from asm, the loads are the
+// caller's to wait for (s_waitcnt vmcnt and a barrier before the
+// destination is read).  The s_nop is the wait state between writing M0
+// and the load that reads it.
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds_addr) {
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_addr);  // uniform: already scalar, or one readlane
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0v)
+                 : "memory", "m0");
+}
+
 // max and sum of x over lanes l and l ^ 32 (symmetric, so the result does
 // not depend on which operand receives which half).
 __device__ __forceinline__ float max_pair32(float x) {

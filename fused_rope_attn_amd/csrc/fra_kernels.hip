@@ -12,12 +12,15 @@
 //                  rescaling is needed.
 //   long_kernel    segments of any length (full-attention layers).  Split-Q
 //                  flash tiling: an 8-wave workgroup owns 256 query rows of
-//                  one (segment, head); K, V and the cos/sin rows of each
-//                  64-key block are staged in LDS by direct loads, K is rotated
-//                  once per block there, and each wave runs an exp2 online
-//                  softmax over its 32 rows.  A partly filled last round of
-//                  workgroups is split along the key range and merged by
-//                  split_merge_kernel.
+//                  one (segment, head); each wave runs an exp2 online softmax
+//                  over its 32 rows.  With a workspace, krot_kernel first
+//                  writes K rotated for the whole call and the K_rot and V
+//                  blocks are staged in LDS by direct loads, with the two
+//                  wavefronts of a SIMD half an iteration apart (ping-pong);
+//                  without one, raw K and the cos/sin rows are staged and K
+//                  is rotated once per block in LDS.  A partly filled last
+//                  round of workgroups is split along the key range and
+//                  merged by split_merge_kernel.
 //
 // Both can also write the softmax log-sum-exp for the backward (fra_bwd.hip).
 //
@@ -780,8 +783,9 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     typedef short v4i16 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
     typedef __attribute__((address_space(3))) void lds_void;
-    typedef __attribute__((address_space(1))) void glb_void;
     __shared__ __attribute__((aligned(16))) char lds[LDS::kBytes];
+    // LDS byte address of lds + off (the direct loads' destination register)
+    auto lds_addr = [&](uint32_t off) { return (uint32_t)(uintptr_t)(lds_void *)(lds + off); };
 
     // Unit u = (segment, head, query block); workgroups past tail_first take
     // part `part` of the key range of a unit of the split last round.
@@ -963,8 +967,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         if (jb.col != kPadSlot) {
             const uint32_t voff = (uint32_t)min(jb.row, nkv - 1) * jb.rows + jb.col;
             const char *src = jb.base + (int64_t)x * kLongBKV * jb.rows;
-            __builtin_amdgcn_global_load_lds((glb_void *)(src + voff), (lds_void *)(lds + jb.lds0 + bf * jb.bufstep),
-                                             16, 0, 0);
+            dma16(src + voff, lds_addr(jb.lds0 + bf * jb.bufstep));
         }
     };
     // The loads of iteration j (generic path).
@@ -978,7 +981,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     uint32_t jstep[MPER], jdst[MPER][2], jvoff[MPER];
     auto job_steady = [&](int m, int P) {
         if (jvoff[m] != kPadSlot)
-            __builtin_amdgcn_global_load_lds((glb_void *)(jptr[m] + jvoff[m]), (lds_void *)(lds + jdst[m][P]), 16, 0, 0);
+            dma16(jptr[m] + jvoff[m], lds_addr(jdst[m][P]));
         jptr[m] += jstep[m];
     };
 
@@ -1193,21 +1196,12 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     // (P = parity of j) may assume blocks j..j+DIST exist and are full, and
     // keeps phases A and B in one basic block so that the compiler can overlap
     // the MFMAs with the softmax and rotation work; the generic variant checks.
-    auto iteration_steady = [&](auto par_tag, int j, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
-        constexpr int P = decltype(par_tag)::value;
-        smax(cur, kLongBKV);
-        constexpr int RB2 = RAWBUFS == 2 ? P : 0;  // raw buffer of block j + 2
-#pragma unroll
-        for (int m = 0; m < MFULL; ++m) job_steady(m, P);
-        if constexpr (RAWBUFS == 1 && MPER > MFULL) {
-            // one raw buffer: every load of the iteration precedes the mid barrier
-            if (has_job(MFULL)) job_steady(MFULL, P);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        // Phase A, one MFMA of S(j+1) then about three exponentials of S(j)
-        // per step, so that the matrix core and the vector unit of this
-        // wave both stay busy (the two accumulator chains alternate, and the
-        // K_rot operand of a step is read two steps ahead).
+    // Phase A of iteration j: S(j+1) on the matrix core, one MFMA then about
+    // three exponentials of S(j) per step, so that the matrix core and the
+    // vector unit of this wave both stay busy (the two accumulator chains
+    // alternate, and the K_rot operand of a step is read two steps ahead);
+    // then P(j) packed as the B operands of the four PV steps.
+    auto phase_a = [&](int j, f32x16 (&cur)[2], f32x16 (&nxt)[2], u32x4 (&pop)[4]) {
         {
             constexpr int NA = 2 * S;
             const char *kb = lds + k_lane + ((j + 1) & 1) * LDS::kKrot;
@@ -1231,7 +1225,6 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
             }
             if constexpr (!ONES) l_i += sum_pair32(lsum);
         }
-        u32x4 pop[4];
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
 #pragma unroll
@@ -1241,6 +1234,20 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
                                        E::pack(cur[a][8 * h + 4], cur[a][8 * h + 5]),
                                        E::pack(cur[a][8 * h + 6], cur[a][8 * h + 7])};
         }
+    };
+    auto iteration_steady = [&](auto par_tag, int j, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+        constexpr int P = decltype(par_tag)::value;
+        smax(cur, kLongBKV);
+        constexpr int RB2 = RAWBUFS == 2 ? P : 0;  // raw buffer of block j + 2
+#pragma unroll
+        for (int m = 0; m < MFULL; ++m) job_steady(m, P);
+        if constexpr (RAWBUFS == 1 && MPER > MFULL) {
+            // one raw buffer: every load of the iteration precedes the mid barrier
+            if (has_job(MFULL)) job_steady(MFULL, P);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        u32x4 pop[4];
+        phase_a(j, cur, nxt, pop);
         if constexpr (RAWBUFS == 1) {
             wait_dma();
             __syncthreads();
@@ -1279,7 +1286,10 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     // Steady iterations j need blocks up to j + DIST to exist and be full:
     // j + DIST < nblk - 1, i.e. j < nblk - DIST - 1; taken in pairs.
     int j = 0;
-    if (nblk - DIST - 1 >= 2) {
+    const int nsteady = nblk - DIST - 1;
+    if (nsteady >= 2) {
+        bool kjob[MPER];  // job m is a K_rot (raw) job, else a V job
+        int nk = 0, nv = 0;
 #pragma unroll
         for (int m = 0; m < MPER; ++m) {
             Job jb;
@@ -1291,10 +1301,71 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
 #pragma unroll
             for (int P = 0; P < 2; ++P)
                 jdst[m][P] = jb.lds0 + (jb.raw ? (uint32_t)((P + DIST) % RAWBUFS) : (uint32_t)((P + 1) & 1)) * jb.bufstep;
+            kjob[m] = jb.raw;
+            if (has_job(m)) {
+                nk += jb.raw ? 1 : 0;
+                nv += jb.raw ? 0 : 1;
+            }
         }
-        for (; j + 1 < nblk - DIST - 1; j += 2) {
-            iteration_steady(Even{}, j, sA, sB);
-            iteration_steady(Odd{}, j + 1, sB, sA);
+        if constexpr (PRE) {
+            // Ping-pong: wavefronts 0-3 and 4-7 (one of each per SIMD) run
+            // half an iteration apart, with a barrier per half-iteration, so
+            // that one wavefront of a SIMD does phase A (QK^T MFMAs beside
+            // the exponentials) while the other does phase B (the PV MFMAs).
+            // Group 0 runs A(j) in half-iteration 2j and B(j) in 2j + 1;
+            // group 1 one half later.  Every wavefront issues its K_rot(j+2)
+            // jobs at the start of half-iteration 2j (K_rot(j)'s buffer was
+            // last read in 2j - 1) and its V(j+1) jobs at the start of 2j + 1
+            // (V(j-1)'s buffer was last read in 2j), and ends each
+            // half-iteration waiting for the jobs it issued in the one
+            // before: what a half-iteration reads was loaded two halves
+            // earlier and is behind a barrier.  Block j + 2 of the last
+            // steady iteration's K_rot jobs is the generic loop's.
+            static_assert(kLongWaves == 8, "two groups of one wavefront per SIMD");
+            const int grp = w >> 2;
+            // s_waitcnt takes an immediate; more outstanding jobs than the
+            // largest case only wait longer.
+            auto half_barrier = [](int keep) {
+                if (keep <= 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                else if (keep == 1) asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                else if (keep == 2) asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                else asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            };
+            auto issue = [&](bool kind, int par) {  // this wavefront's jobs of one kind, buffer parity par
+#pragma unroll
+                for (int m = 0; m < MPER; ++m) {
+                    if (has_job(m) && kjob[m] == kind) {
+                        if (jvoff[m] != kPadSlot) dma16(jptr[m] + jvoff[m], lds_addr(par ? +jdst[m][1] : +jdst[m][0]));
+                        jptr[m] += jstep[m];
+                    }
+                }
+            };
+            auto iteration_pp = [&](auto par_tag, int jj, f32x16 (&cur)[2], f32x16 (&nxt)[2], bool more) {
+                constexpr int P = decltype(par_tag)::value;
+                u32x4 pop[4];
+                issue(grp == 0, P);  // group 0: K_rot(jj+2); group 1: V(jj+1)
+                smax(cur, kLongBKV);
+                phase_a(jj, cur, nxt, pop);
+                half_barrier(grp == 0 ? nk : nv);
+                if (grp == 0) issue(false, P);      // V(jj+1)
+                else if (more) issue(true, P ^ 1);  // K_rot(jj+3)
+                pv(jj, pop);
+                half_barrier(grp == 0 ? nv : (more ? nk : 0));
+            };
+            if (grp == 1) {  // K_rot(2), which group 0 issues with A(0)
+                issue(true, 0);
+                half_barrier(nk);
+            }
+            for (; j + 1 < nsteady; j += 2) {
+                iteration_pp(Even{}, j, sA, sB, true);
+                iteration_pp(Odd{}, j + 1, sB, sA, j + 3 < nsteady);
+            }
+            if (grp == 0) half_barrier(0);  // group 1 finishes B of the last steady iteration
+        } else {
+            for (; j + 1 < nsteady; j += 2) {
+                iteration_steady(Even{}, j, sA, sB);
+                iteration_steady(Odd{}, j + 1, sB, sA);
+            }
         }
     }
     for (; j < nblk; j += 2) {
