@@ -783,6 +783,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     typedef short v4i16 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
     typedef __attribute__((address_space(3))) void lds_void;
+    typedef __attribute__((address_space(1))) void glb_void;
     __shared__ __attribute__((aligned(16))) char lds[LDS::kBytes];
     // LDS byte address of lds + off (the direct loads' destination register)
     auto lds_addr = [&](uint32_t off) { return (uint32_t)(uintptr_t)(lds_void *)(lds + off); };
@@ -967,7 +968,10 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         if (jb.col != kPadSlot) {
             const uint32_t voff = (uint32_t)min(jb.row, nkv - 1) * jb.rows + jb.col;
             const char *src = jb.base + (int64_t)x * kLongBKV * jb.rows;
-            dma16(src + voff, lds_addr(jb.lds0 + bf * jb.bufstep));
+            // (the compiler's own direct load: a generic iteration's
+            // transposed reads may wait for it, the steady loops' may not)
+            __builtin_amdgcn_global_load_lds((glb_void *)(src + voff), (lds_void *)(lds + jb.lds0 + bf * jb.bufstep),
+                                             16, 0, 0);
         }
     };
     // The loads of iteration j (generic path).

@@ -365,11 +365,15 @@ def test_long_kernel_split_last_round(device, lens, h, d):
     ([700, 1500, 64, 1], 2, 72, torch.float32, True),
     ([520, 130], 3, 64, torch.bfloat16, False),
     ([333], 2, 128, torch.float16, True),
+    # 5, 7, 8, 9 and 16 key blocks: 2, 4, 5, 6 and 13 steady iterations (the
+    # ping-pong loop runs them in pairs, the rest go to the generic loop)
+    ([257, 385, 449, 513, 1024, 3], 2, 80, torch.float32, False),
 ])
 def test_long_kernel_rotated_k_workspace(device, lens, h, d, rope_dtype, full):
     # K rotated once per call into the workspace (a separate kernel) and then
-    # staged, against K rotated per block inside the kernel: both round the
-    # same fp32 rotation to the storage dtype, so the outputs are identical
+    # staged by the ping-pong loop, against K rotated per block inside the
+    # kernel by the lockstep loop: both round the same fp32 rotation to the
+    # storage dtype and sum in the same order, so the outputs are identical
     case = random_case(lens, h=h, d=d, seed=270 + d, rope_dtype=rope_dtype, width=d if full else d // 2)
     pre, pl = _call_abi(case, device, workspace="krot")
     inkernel, pl0 = _call_abi(case, device, workspace=False)
