@@ -392,7 +392,6 @@ __device__ __forceinline__ void bwd_dq_unit(const BParams &p, char *lds, int uni
     // a wavefront that is ahead stores the next block while the others still
     // read the current one; one barrier per block.
     auto store_block = [&](int kb) {
-        const int nk = min(BKV, L - kb * BKV);
         const int ft = fresh(tid);
         char *const base = lds + (kb & 1) * LDS::kStage;
         kbk.store(base + kKr, PTR, ft);
@@ -551,7 +550,6 @@ __device__ __forceinline__ void bwd_dkdv_unit(const BParams &p, char *lds, int u
     // a wavefront that is ahead stores the next block while the others still
     // read the current one; one barrier per block.
     auto store_block = [&](int qb) {
-        const int nq = min(BQ, L - qb * BQ);
         const int ft = fresh(tid);
         char *const base = lds + (qb & 1) * LDS::kStage;
         qbk.store(base + kQr, PTR, ft);

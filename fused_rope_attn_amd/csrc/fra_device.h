@@ -114,12 +114,19 @@ __device__ __forceinline__ void permlane32_swap(float &a, float &b) {
 // transposed LDS read wait (vmcnt(0)) for every direct load in flight,
 // whichever buffer either touches; issued from asm, the loads are the
 // caller's to wait for (s_waitcnt vmcnt and a barrier before the
-// destination is read).  The s_nop is the wait state between writing M0
-// and the load that reads it.
+// destination is read).  M0 is a reserved register, which a clobber list
+// does not protect, so the asm saves and restores it; the s_nops are the
+// wait states between writing M0 and the load that reads it, and between
+// the load and the restore.
 __device__ __forceinline__ void dma16(const void *src, uint32_t lds_addr) {
     const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_addr);  // uniform: already scalar, or one readlane
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0v)
-                 : "memory", "m0");
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+        "s_nop 0\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(src), "s"(m0v)
+        : "memory");
 }
 
 // max and sum of x over lanes l and l ^ 32 (symmetric, so the result does

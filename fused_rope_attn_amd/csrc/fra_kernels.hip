@@ -834,7 +834,7 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
 
     // V padding columns [D, 32*NDT) of both buffers: zero, column D ones.
     // They are never overwritten by the staging loads.
-    {
+    if constexpr (VPC > KCH) {
         constexpr int PADC = VPC - KCH;  // padding chunks of a V row
         const u32 one = E::pack(1.0f, 0.0f) & 0xffffu;
         for (int i = tid; i < 2 * 64 * PADC; i += kLongThreads) {
