@@ -233,7 +233,8 @@ def _prepare(q, k, v, cos, sin, long_kernel: bool):
 
 
 def _workspace_bytes(lib, args) -> int:
-    """Bytes of the long kernel's optional workspace (0: no split applies)."""
+    """Bytes of the long kernel's optional workspace: rotated K and the split
+    scratch (0 for the window kernel)."""
     total = ctypes.c_int64(0)
     _lib.check(lib.fra_workspace_bytes(args, ctypes.byref(total)))
     return int(total.value)
@@ -322,10 +323,11 @@ def _forward(q, k, v, cos, sin, cu, max_seqlen: int, scale: float, out, lse):
         args.lse = lse.data_ptr()
     ws = None
     with torch.cuda.device(q.device):
-        # The long kernel splits a partly filled last round of workgroups
-        # along the key range when given a workspace (scratch, per call, from
-        # torch's caching allocator: stream-ordered reuse keeps it alive for
-        # the kernels that use it).
+        # The long kernel's workspace (scratch, per call, from torch's
+        # caching allocator: stream-ordered reuse keeps it alive for the
+        # kernels that use it) holds K rotated once per call and, where a
+        # partly filled last round of workgroups is split along the key
+        # range, the parts' partial rows.
         nbytes = _workspace_bytes(lib, args)
         if nbytes:
             ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
