@@ -255,7 +255,10 @@ def test_deterministic(device):
 
 
 def test_graph_capture_replays(device):
-    case = random_case([64, 64, 30, 150], h=4, d=80, seed=1000)
+    # 700 tokens: the long kernel with K rotated into the captured workspace
+    # and the ping-pong loop; K changes between replays, so a stale rotated
+    # K would show
+    case = random_case([64, 64, 30, 700], h=4, d=80, seed=1000)
     st = {k: (v.to(device) if torch.is_tensor(v) else v) for k, v in case.items()}
     out = torch.empty_like(st["q"])
     ms = case["max_seqlen"]
@@ -273,8 +276,8 @@ def test_graph_capture_replays(device):
         call()
     g = torch.Generator().manual_seed(1001)
     for _ in range(4):
-        st["q"].copy_(torch.randn(st["q"].shape, generator=g).to(st["q"].dtype))
-        st["v"].copy_(torch.randn(st["v"].shape, generator=g).to(st["v"].dtype))
+        for x in ("q", "k", "v"):
+            st[x].copy_(torch.randn(st[x].shape, generator=g).to(st[x].dtype))
         graph.replay()
         torch.cuda.synchronize()
         got = out.clone()
