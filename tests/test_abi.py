@@ -164,6 +164,27 @@ def test_forward_workspace_size_and_alignment():
     assert "workspace" in lib.fra_last_error().decode()
 
 
+@pytest.mark.parametrize("seglen,nseg,parts", [
+    (9216, 1, 4),   # 576 units: a last round of 64 on 256 CUs, 144 key blocks per unit
+    (2304, 8, 2),   # 1152 units: 128 left over, 2 parts of 18 key blocks
+    (512, 18, 0),   # 576 units, but 8 key blocks per unit: parts of 4 or 2 blocks lose
+    (256, 36, 0),
+])
+def test_split_plan_needs_eight_key_blocks_per_part(seglen, nseg, parts):
+    # CU count assumed 256 without a GPU; the workspace holds everything asked for
+    lib = _lib.load()
+    n = seglen * nseg
+    a = make_args(n=n, nseg=nseg, max_seqlen=seglen, num_seqs=nseg)
+    nbytes = ctypes.c_int64(0)
+    assert lib.fra_workspace_bytes(a, ctypes.byref(nbytes)) == _lib.FRA_OK
+    a.workspace, a.workspace_bytes = (1 << 20) * 10, nbytes.value
+    rc, p = plan_of(a)
+    assert rc == _lib.FRA_OK and p.kernel == _lib.FRA_KERNEL_LONG
+    assert p.split_parts == parts
+    if parts:
+        assert p.split_units == (16 * nseg * (seglen // 256)) % 256
+
+
 def make_bwd_args(**kw):
     a = _lib.BwdArgs()
     n, h, d = kw.get("n", 1024), kw.get("h", 16), kw.get("d", 80)
