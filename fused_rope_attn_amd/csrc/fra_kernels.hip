@@ -670,8 +670,8 @@ constexpr int kSplitMinBlocks = 8;  // key blocks per part, at least
 
 __host__ __device__ constexpr int split_row_floats(int d) { return (d + 2 + 3) / 4 * 4; }  // 16-byte pitch
 
-// Workgroups (of 256 threads, one per (row, 4 columns)) of the merge per unit.
-__host__ __device__ constexpr int split_merge_blocks(int d) { return (kLongBQ * (d / 4) + 255) / 256; }
+// Workgroups (of 256 threads, one per (row, 8 columns)) of the merge per unit.
+__host__ __device__ constexpr int split_merge_blocks(int d) { return (kLongBQ * (d / 8) + 255) / 256; }
 
 inline int64_t split_workspace_bytes(int64_t units, int parts, int d) {
     return units * parts * kLongBQ * (int64_t)split_row_floats(d) * 4;
@@ -703,15 +703,17 @@ __device__ __forceinline__ void split_write_partial(const KParams &p, int u, int
 }
 
 // O = sum_p 2^(m_p - m) O_p / sum_p 2^(m_p - m) l_p with m = max_p m_p,
-// rounded to the output dtype.  Items are (row, 4-column chunk) of a split
+// rounded to the output dtype.  Items are (row, 8-column chunk) of a split
 // unit, one per thread (consecutive threads on consecutive chunks of a row):
-// workgroup (tu, blk) of the grid split_units x (head_dim / 4) takes items
-// 256 blk .. 256 blk + 255 of unit tu.
+// workgroup (tu, blk) of the grid split_units x split_merge_blocks takes
+// items 256 blk .. 256 blk + 255 of unit tu.
 template <int D, class E>
 __global__ __launch_bounds__(256) void split_merge_kernel(const KParams p) {
     constexpr int RF = split_row_floats(D);
-    constexpr int NC = D / 4;
+    static_assert(D % 8 == 0, "8-column items");
+    constexpr int NC = D / 8;
     constexpr int BPU = split_merge_blocks(D);  // workgroups per unit
+    typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
     const int tu = blockIdx.x / BPU, blk = blockIdx.x - tu * BPU;
     const int u = p.tail_first + tu, nparts = p.tail_split;
     const int sh = u / p.qblocks, qblk = u - sh * p.qblocks;
@@ -727,14 +729,16 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const KParams p) {
     if (L <= 0 || q >= L) return;
     const float *base = (const float *)p.ws + ((int64_t)tu * nparts * kLongBQ + row) * RF;
     float mp[kSplitMaxParts], lp[kSplitMaxParts];
-    f32x4 op[kSplitMaxParts];
+    f32x4 op[kSplitMaxParts][2];
 #pragma unroll
     for (int pp = 0; pp < kSplitMaxParts; ++pp) {
         if (pp < nparts) {
             const float *pr = base + (int64_t)pp * kLongBQ * RF;
-            mp[pp] = pr[D];
-            lp[pp] = pr[D + 1];
-            op[pp] = *(const f32x4 *)(pr + 4 * c);
+            const f32x2 ml = *(const f32x2 *)(pr + D);  // D % 8 == 0: 8-byte aligned
+            mp[pp] = ml[0];
+            lp[pp] = ml[1];
+            op[pp][0] = *(const f32x4 *)(pr + 8 * c);
+            op[pp][1] = *(const f32x4 *)(pr + 8 * c + 4);
         }
     }
     float mx = kNegInf;
@@ -742,19 +746,22 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const KParams p) {
     for (int pp = 0; pp < kSplitMaxParts; ++pp)
         if (pp < nparts) mx = fmaxf(mx, mp[pp]);
     float l = 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
 #pragma unroll
     for (int pp = 0; pp < kSplitMaxParts; ++pp) {
         if (pp < nparts && mp[pp] != kNegInf) {  // a part with no keys adds nothing
             const float wt = __builtin_amdgcn_exp2f(mp[pp] - mx);
             l += wt * lp[pp];
-            acc += wt * op[pp];
+            acc0 += wt * op[pp][0];
+            acc1 += wt * op[pp][1];
         }
     }
     const float inv = 1.0f / l;
     if (p.lse != nullptr && c == 0) p.lse[(int64_t)head * p.total + s0 + q] = (mx + __builtin_amdgcn_logf(l)) * kLn2;
     char *orow = p.out + ((int64_t)(s0 + q) * p.so_s + (int64_t)head * p.so_h) * 2;
-    *(u32x2 *)(orow + 8 * c) = u32x2{E::pack(acc[0] * inv, acc[1] * inv), E::pack(acc[2] * inv, acc[3] * inv)};
+    *(u32x2 *)(orow + 16 * c) = u32x2{E::pack(acc0[0] * inv, acc0[1] * inv), E::pack(acc0[2] * inv, acc0[3] * inv)};
+    *(u32x2 *)(orow + 16 * c + 8) =
+        u32x2{E::pack(acc1[0] * inv, acc1[1] * inv), E::pack(acc1[2] * inv, acc1[3] * inv)};
 }
 
 template <int D, class E, int RD, bool FULL, bool PRE>
