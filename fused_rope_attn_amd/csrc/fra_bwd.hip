@@ -64,6 +64,7 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
 __host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
+__host__ __device__ constexpr int cmin(int a, int b) { return a < b ? a : b; }
 __host__ __device__ constexpr int bwd_dp(int d) { return (d + 15) / 16 * 16; }
 
 // LDS row pitch (bytes) of a region read both as rows (16-byte reads) and
@@ -679,22 +680,30 @@ void bwd_long_kernel(const BParams p) {
 //   phase 2  wave w owns keys 32w..32w+31 (the dk/dv kernel's layout): S, dP,
 //            dZ, dV^T = dO^T P and dK^T = Q_rot^T dZ; dv is stored from
 //            registers and dk's rows go through LDS for the inverse rotation.
-template <int D> struct WinBwdLds {
+// VREG = false: V is staged too; dQ's fp32 rows go over K_rot + V after
+// phase 1, dK's after them at the end.  VREG = true: a lane's rows of V come
+// from HBM as registers, and dQ's then dK's fp32 rows go over the dead
+// staging one after the other at the end, so that four workgroups fit on a
+// CU at D <= 96 instead of three.  Which pays depends on the grid: four per
+// CU took a 1024-workgroup layer (cfg1) from two rounds to one (38 -> 32 µs)
+// but made a 2304-workgroup one (cfg2w) 5% slower, so the host takes VREG
+// only when the grid fits four per CU and not three.
+template <int D, bool VREG> struct WinBwdLds {
     static constexpr int PTR = bwd_pitch_tr(D), PRD = bwd_pitch_rows(D), FP = bwd_pitch_f32(D);
-    static constexpr int kKr = 0, kV = 64 * PTR, kQr = kV + 64 * PRD, kDo = kQr + 64 * PTR;
+    static constexpr int kKr = 0, kV = 64 * PTR, kQr = kV + (VREG ? 0 : 64 * PRD), kDo = kQr + 64 * PTR;
     static constexpr int kLse = kDo + 64 * PTR, kDvec = kLse + 64 * 4;
     static constexpr int kStage = kDvec + 64 * 4;
-    // fp32 rows of dQ over K_rot + V (dead once phase 1 holds its operands),
-    // then those of dK after it (over Q_rot and dO, dead after phase 2).
-    static constexpr int kFq = 0, kFk = 64 * FP;
-    static_assert(64 * FP <= kQr, "dQ rows must fit over the K_rot and V staging");
-    static constexpr int kBytes = cmax(kStage, 2 * 64 * FP);
+    static constexpr int kFq = 0, kFk = VREG ? 0 : 64 * FP;
+    static_assert(VREG || 64 * FP <= kQr, "dQ rows must fit over the K_rot and V staging");
+    static constexpr int kBytes = cmax(kStage, (VREG ? 1 : 2) * 64 * FP);
+    // Workgroups (two wavefronts) per CU: LDS and the waves-per-SIMD budget.
+    static constexpr int kPerCu = cmin(160 * 1024 / kBytes, 4 * BwdOcc<D>::kWaves / 2);
 };
 
-template <int D, class E, bool FULL>
+template <int D, class E, bool FULL, bool VREG>
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(BwdOcc<D>::kWaves, BwdOcc<D>::kWaves)))
 void bwd_window_kernel(const BParams p) {
-    using LDS = WinBwdLds<D>;
+    using LDS = WinBwdLds<D, VREG>;
     constexpr int DP = bwd_dp(D), S = DP / 16, NDT = (D + 31) / 32;
     constexpr int PTR = LDS::PTR, PRD = LDS::PRD, FP = LDS::FP;
     constexpr int NT = 128;
@@ -716,13 +725,31 @@ void bwd_window_kernel(const BParams p) {
     // Every load of the workgroup first (one HBM round trip), then the
     // rotations and LDS writes.  q and k share their cos/sin loads.
     u32x4 orow[S];  // this lane's row of out, for Dvec in phase 1
+    // VREG: V rows 32a + r, elements 16t + 8g..: the A operands of dP^T in
+    // phase 1, and (a = w) this lane's key row, the B operand of dP in phase 2.
+    u32x4 va[VREG ? 2 : 1][S];
     {
         RotBlock<D, E, FULL, 64, NT, 2> qk;
-        RowBlock<D, 64, NT> vb, db;
+        RowBlock<D, VREG ? 1 : 64, NT> vb;
+        RowBlock<D, 64, NT> db;
         const char *const x[2] = {p.q + qoff, p.k + koff};
         const int64_t xs[2] = {p.sq_s * 2, p.sk_s * 2};
         qk.load(p, x, xs, s0, L, tid);
-        vb.load(p.v + ((int64_t)s0 * p.sv_s + (int64_t)head * p.sv_h) * 2, p.sv_s * 2, L, tid);
+        const char *vbase = p.v + ((int64_t)s0 * p.sv_s + (int64_t)head * p.sv_h) * 2;
+        if constexpr (VREG) {
+#pragma unroll
+            for (int a = 0; a < 2; ++a) {
+                const int vr = 32 * a + r;
+#pragma unroll
+                for (int t = 0; t < S; ++t) {
+                    const int d0 = 16 * t + 8 * g;
+                    va[a][t] = (vr < L && d0 < D) ? *(const u32x4 *)(vbase + (int64_t)vr * p.sv_s * 2 + 2 * d0)
+                                                  : u32x4{0u, 0u, 0u, 0u};
+                }
+            }
+        } else {
+            vb.load(vbase, p.sv_s * 2, L, tid);
+        }
         db.load(p.dout + ((int64_t)s0 * p.sdo_s + (int64_t)head * p.sdo_h) * 2, p.sdo_s * 2, L, tid);
         const char *op = p.out + ((int64_t)(s0 + (rvalid ? row : 0)) * p.so_s + (int64_t)head * p.so_h) * 2;
 #pragma unroll
@@ -734,7 +761,7 @@ void bwd_window_kernel(const BParams p) {
         const float lv = tid < L ? p.lse[(int64_t)head * p.total + s0 + tid] * kLog2e : __builtin_inff();
         char *const dst[2] = {lds + LDS::kQr, lds + LDS::kKr};
         qk.store(dst, PTR, L, tid);
-        vb.store(lds + LDS::kV, PRD, tid);
+        if constexpr (!VREG) vb.store(lds + LDS::kV, PRD, tid);
         db.store(lds + LDS::kDo, PTR, tid);
         if (tid < 64) ((float *)(lds + LDS::kLse))[tid] = lv;
     }
@@ -776,9 +803,13 @@ void bwd_window_kernel(const BParams p) {
                         sacc[a] = E::mma(*(const u32x4 *)(lds + LDS::kKr + (32 * a + r) * PTR + 32 * t + 16 * g),
                                          qop[t], sacc[a]);
 #pragma unroll
-                    for (int t = 0; t < S; ++t)
-                        dpacc[a] = E::mma(*(const u32x4 *)(lds + LDS::kV + (32 * a + r) * PRD + 32 * t + 16 * g),
-                                          dop[t], dpacc[a]);
+                    for (int t = 0; t < S; ++t) {
+                        if constexpr (VREG)
+                            dpacc[a] = E::mma(va[a][t], dop[t], dpacc[a]);
+                        else
+                            dpacc[a] = E::mma(*(const u32x4 *)(lds + LDS::kV + (32 * a + r) * PRD + 32 * t + 16 * g),
+                                              dop[t], dpacc[a]);
+                    }
                 }
             }
             u32x4 dsop[2][2];
@@ -805,27 +836,34 @@ void bwd_window_kernel(const BParams p) {
             }
         }
     }
-    // Phase 2's B operands (this lane's key row of K_rot and V) before their
-    // LDS is reused.
+    // Phase 2's B operands: this lane's key row of K_rot, and of V (VREG:
+    // tile w of the phase-1 operands, a select of values, not of the array
+    // slots), before their LDS is reused.
     u32x4 kop[S], vop[S];
 #pragma unroll
     for (int t = 0; t < S; ++t) {
         kop[t] = *(const u32x4 *)(lds + LDS::kKr + row * PTR + 32 * t + 16 * g);
-        vop[t] = *(const u32x4 *)(lds + LDS::kV + row * PRD + 32 * t + 16 * g);
+        if constexpr (VREG) vop[t] = w ? +va[VREG ? 1 : 0][t] : +va[0][t];
+        else vop[t] = *(const u32x4 *)(lds + LDS::kV + row * PRD + 32 * t + 16 * g);
     }
-    __syncthreads();  // K_rot and V are dead; Dvec is complete
-    float *fq = (float *)(lds + LDS::kFq);
+    __syncthreads();  // Dvec is complete (and, without VREG, K_rot and V are dead)
+    // fp32 rows of dQ_rot, then of dK_rot, each followed by the inverse
+    // rotation and the store.
+    auto rows_out = [&](float *f, const f32x16 (&acc)[NDT]) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
+        for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
-        for (int jq = 0; jq < 4; ++jq) {
-            const int d0 = 32 * dt + 8 * jq + 4 * g;
-            if (d0 < D)
-                *(f32x4 *)(fq + row * (FP / 4) + d0) =
-                    f32x4{dqacc[dt][4 * jq + 0], dqacc[dt][4 * jq + 1], dqacc[dt][4 * jq + 2], dqacc[dt][4 * jq + 3]} *
-                    p.scale;
+            for (int jq = 0; jq < 4; ++jq) {
+                const int d0 = 32 * dt + 8 * jq + 4 * g;
+                if (d0 < D)
+                    *(f32x4 *)(f + row * (FP / 4) + d0) =
+                        f32x4{acc[dt][4 * jq + 0], acc[dt][4 * jq + 1], acc[dt][4 * jq + 2], acc[dt][4 * jq + 3]} *
+                        p.scale;
+            }
         }
-    }
+    };
+    float *fq = (float *)(lds + LDS::kFq), *fk = (float *)(lds + LDS::kFk);
+    if constexpr (!VREG) rows_out(fq, dqacc);
 
     // ---- phase 2: dK, dV for keys 32w..32w+31 ----------------------------------------
     f32x16 dvacc[NDT], dkacc[NDT];
@@ -889,21 +927,20 @@ void bwd_window_kernel(const BParams p) {
         }
     }
     __syncthreads();  // Q_rot and dO are dead
-    float *fk = (float *)(lds + LDS::kFk);
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-        for (int jq = 0; jq < 4; ++jq) {
-            const int d0 = 32 * dt + 8 * jq + 4 * g;
-            if (d0 < D)
-                *(f32x4 *)(fk + row * (FP / 4) + d0) =
-                    f32x4{dkacc[dt][4 * jq + 0], dkacc[dt][4 * jq + 1], dkacc[dt][4 * jq + 2], dkacc[dt][4 * jq + 3]} *
-                    p.scale;
-        }
+    if constexpr (VREG) {
+        rows_out(fq, dqacc);
+        __syncthreads();
+        unrotate_store<D, E, FULL>(fq, FP / 4, p, p.dq + ((int64_t)s0 * p.sdq_s + (int64_t)head * p.sdq_h) * 2,
+                                   p.sdq_s * 2, s0, L, tid, NT);
+        __syncthreads();  // dQ's rows are read
+        rows_out(fk, dkacc);
+        __syncthreads();
+    } else {
+        rows_out(fk, dkacc);
+        __syncthreads();
+        unrotate_store<D, E, FULL>(fq, FP / 4, p, p.dq + ((int64_t)s0 * p.sdq_s + (int64_t)head * p.sdq_h) * 2,
+                                   p.sdq_s * 2, s0, L, tid, NT);
     }
-    __syncthreads();
-    unrotate_store<D, E, FULL>(fq, FP / 4, p, p.dq + ((int64_t)s0 * p.sdq_s + (int64_t)head * p.sdq_h) * 2,
-                               p.sdq_s * 2, s0, L, tid, NT);
     unrotate_store<D, E, FULL>(fk, FP / 4, p, p.dk + ((int64_t)s0 * p.sdk_s + (int64_t)head * p.sdk_h) * 2,
                                p.sdk_s * 2, s0, L, tid, NT);
 }
@@ -915,13 +952,25 @@ typedef void (*BwdFn)(BParams);
 struct BwdKernels {
     BwdFn dot, rotate, matrix;  // longer segments: Dvec, q_rot / k_rot, then dq and dk/dv units
     int nw;
-    BwdFn window;  // every segment <= 64 tokens: the one-pass kernel
+    BwdFn window;       // every segment <= 64 tokens: the one-pass kernel, V staged
+    BwdFn window_vreg;  // ... V in registers (four workgroups per CU where three fit otherwise)
+    int per_cu, per_cu_vreg;
 };
 
 template <int D, class E, bool FULL, int NW>
 BwdKernels bwd_kernels_nw() {
-    return BwdKernels{(BwdFn)bwd_dot_kernel<D, E>, (BwdFn)bwd_rotate_kernel<D, E, FULL>,
-                      (BwdFn)bwd_long_kernel<D, E, FULL, NW>, NW, (BwdFn)bwd_window_kernel<D, E, FULL>};
+    // (no register-V instance at D = 96 with full-width tables: it spills)
+    constexpr bool kVreg = !(D == 96 && FULL);
+    BwdFn vreg = nullptr;
+    if constexpr (kVreg) vreg = (BwdFn)bwd_window_kernel<D, E, FULL, true>;
+    return BwdKernels{(BwdFn)bwd_dot_kernel<D, E>,
+                      (BwdFn)bwd_rotate_kernel<D, E, FULL>,
+                      (BwdFn)bwd_long_kernel<D, E, FULL, NW>,
+                      NW,
+                      (BwdFn)bwd_window_kernel<D, E, FULL, false>,
+                      vreg,
+                      WinBwdLds<D, false>::kPerCu,
+                      kVreg ? WinBwdLds<D, true>::kPerCu : 0};
 }
 
 template <int D, class E>
@@ -1076,7 +1125,11 @@ int fra_bwd_varlen(const fra_bwd_args *a, void *stream) {
     if (a->max_seqlen <= 64) {
         if (sh > 0x7fffffff) return fra_fail(FRA_EUNSUPPORTED, "grid of %lld workgroups is too large", (long long)sh);
         p.blocks = 1;
-        hipLaunchKernelGGL(k.window, dim3((unsigned)sh), dim3(128), 0, st, p);
+        // V in registers only where its fourth workgroup per CU makes the
+        // grid fit in one round that the staged layout would not.
+        const int64_t cus = device_cus();
+        const bool vreg = k.window_vreg && sh > cus * k.per_cu && sh <= cus * k.per_cu_vreg;
+        hipLaunchKernelGGL(vreg ? k.window_vreg : k.window, dim3((unsigned)sh), dim3(128), 0, st, p);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess)
             return fra_fail(FRA_EHIP, "launch of the window backward kernel failed: %s", hipGetErrorString(e));

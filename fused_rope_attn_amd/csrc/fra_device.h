@@ -129,6 +129,27 @@ __device__ __forceinline__ void dma16(const void *src, uint32_t lds_addr) {
         : "memory");
 }
 
+// Compute units of the current device (host code; cached per device and
+// translation unit; 256 when no device can be queried, e.g. planning on a
+// host without a GPU).
+inline int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            (void)hipGetLastError();
+            n = 256;
+        }
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 // max and sum of x over lanes l and l ^ 32 (symmetric, so the result does
 // not depend on which operand receives which half).
 __device__ __forceinline__ float max_pair32(float x) {

@@ -1450,25 +1450,6 @@ struct Choice {
     char name[64];
 };
 
-// Compute units of the current device (cached per device; 256 when no device
-// can be queried, e.g. planning on a host without a GPU).
-int device_cus() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-        (void)hipGetLastError();
-        return 256;
-    }
-    if (cached[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
-            (void)hipGetLastError();
-            n = 256;
-        }
-        cached[dev] = n;
-    }
-    return cached[dev];
-}
 
 // The long kernel's split last round.  Units (segment, head, query block)
 // run one workgroup per CU; when the last round of workgroups leaves CUs

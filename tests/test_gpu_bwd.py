@@ -93,6 +93,11 @@ CASES = [
     ([200], 1, 96, 96, torch.bfloat16, 0, 0),                 # long, full-width tables
     ([150, 70], 2, 128, None, torch.float16, 0, 0),           # long, head_dim 128, fp16
     ([1000], 1, 80, None, torch.bfloat16, 0, 0),              # long, many key/query blocks
+    # window grids of 768 < segments x heads <= 1024 (256 CUs): the variant
+    # with V in registers, four workgroups per CU
+    ([64] * 52 + [17, 0, 5, 33], 16, 80, None, torch.bfloat16, 0, 0),
+    ([64] * 58 + [40, 2], 16, 72, 72, torch.float16, 0, 2),
+    ([64] * 49 + [1], 16, 64, None, torch.bfloat16, 3, 0),
 ]
 
 
