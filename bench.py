@@ -112,6 +112,22 @@ def backward_call(inp):
     return call
 
 
+def floor_call(inp):
+    """A closure running the box's floor for a window layer's traffic: one
+    elementwise kernel that reads the layer's q, k and v and writes an
+    output of the same shape (``torch.addcmul(q, k, v)``: torch's own
+    vectorised, coalesced elementwise kernel), i.e. the fused op's Q/K/V/O
+    bytes with no attention, no rotation, no tables and no dependent
+    round trips between the loads and the store."""
+    q, k, v = inp["q"], inp["k"], inp["v"]
+    o = torch.empty_like(q)
+
+    def call():
+        torch.addcmul(q, k, v, out=o)
+
+    return call
+
+
 def time_calls(call, steps: int, warmup: int, flush: torch.Tensor) -> dict:
     """Cold (1 GiB read before each call) and warm (back-to-back) timings of
     ``call`` with HIP events on torch's current stream, where the kernels run."""
@@ -316,6 +332,8 @@ def profile_driver(args, flush, dev) -> int:
     out = torch.empty_like(q)
     if args.bwd:
         call = backward_call(inp)
+    elif args.floor:
+        call = floor_call(inp)
     else:
         def call():
             fused_rope_attention(q, k, v, cos, sin, cu, inp["max_seqlen"], out=out)
@@ -337,16 +355,82 @@ def profile_driver(args, flush, dev) -> int:
         nbytes = algorithmic_bytes_bwd(n_tok, w.heads, w.head_dim, q.element_size(), cos.shape[1],
                                        cos.element_size(), len(lens))
         flops = algorithmic_flops_bwd(w.heads, w.head_dim, lens)
+    if args.floor:
+        nbytes = 4 * q.numel() * q.element_size()
     print(json.dumps({"profile_driver": args.workload, "direction": "backward" if args.bwd else "forward",
-                      "kernel": pl["name"], "warmup_calls": 3,
+                      "kernel": "floor: torch.addcmul(q, k, v)" if args.floor else pl["name"], "warmup_calls": 3,
                       "calls": args.profile_calls, "bytes": nbytes, "flops": flops,
                       "copy_bytes_each_way": n}), flush=True)
     return 0
 
 
-def drift_stack(wname: str, device, layers: int = 32, full_layers=(7, 15, 23, 31), seed: int = 7) -> dict:
+def torch_reference_attention(q, k, v, cos, sin, cu, scale: float, mode: str = "fp32"):
+    """The unfused path in plain torch float32 on q's device, for stacks too
+    large for the CPU oracle: split-half rotation (reference
+    fused_attn.py:340-345, 385-390), then per-segment softmax attention.
+    ``mode`` "fp32" is the oracle's fp32 path; "bf16" is its rounding-point
+    model (q_rot, k_rot and the unnormalised P rounded to bf16, the row sum
+    from the unrounded P, the output rounded; oracle/attention.py).  Inputs
+    are float32 ``[N, H, D]``; rows outside every segment come back NaN.
+    ``tests/test_gpu_drift.py`` pins it to the CPU oracle."""
+    import math
+
+    n, h, d = q.shape
+    half = d // 2
+    c0, s0 = cos[:, None, :half], sin[:, None, :half]
+    c1, s1 = (cos[:, None, half:], sin[:, None, half:]) if cos.shape[1] == d else (c0, s0)
+
+    def rot(x):
+        x0, x1 = x[..., :half], x[..., half:]
+        return torch.cat([x0 * c0 - x1 * s0, x0 * s1 + x1 * c1], dim=-1)
+
+    qr, kr = rot(q), rot(k)
+    if mode == "bf16":
+        qr, kr = qr.bfloat16().float(), kr.bfloat16().float()
+    scale_log2 = float(torch.tensor(scale, dtype=torch.float32) * torch.tensor(math.log2(math.e), dtype=torch.float32))
+    out = torch.full_like(q, float("nan"))
+    bounds = [(min(max(a, 0), n), min(max(b, 0), n)) for a, b in zip(cu[:-1].tolist(), cu[1:].tolist())]
+    by_len = {}
+    for a, b in bounds:
+        if b > a:
+            by_len.setdefault(b - a, []).append(a)
+    for L, starts in by_len.items():
+        idx = torch.tensor(starts, device=q.device)[:, None] + torch.arange(L, device=q.device)[None, :]
+        # [segments, H, L, D] blocks, several segments or one head's row chunk at a time
+        per_seg = h * L * L * 4
+        step = max(1, (1 << 30) // per_seg)
+        for i in range(0, len(starts), step):
+            sl = idx[i:i + step]
+            qb, kb, vb = (x[sl].permute(0, 2, 1, 3).contiguous() for x in (qr, kr, v))
+            for hh in range(h) if per_seg > (1 << 30) else [None]:
+                hs = slice(None) if hh is None else slice(hh, hh + 1)
+                kt = kb[:, hs].transpose(-1, -2).contiguous()
+                rows = L if hh is None else max(1, (1 << 30) // (L * 4))
+                for r0 in range(0, L, rows):
+                    qq = qb[:, hs, r0:r0 + rows]
+                    s_ = torch.matmul(qq, kt)
+                    if mode == "fp32":
+                        o = torch.matmul(torch.softmax(s_ * scale, dim=-1), vb[:, hs])
+                    else:
+                        s_ = s_ * scale_log2
+                        p_ = torch.exp2(s_ - s_.amax(dim=-1, keepdim=True))
+                        o = torch.matmul(p_.bfloat16().float(), vb[:, hs]) / p_.sum(dim=-1, keepdim=True)
+                    blk = o.permute(0, 2, 1, 3)                   # [segments, rows, heads, D]
+                    tgt = sl[:, r0:r0 + rows]
+                    if hh is None:
+                        out[tgt] = blk
+                    else:
+                        out[tgt, hh:hh + 1] = blk
+    if mode == "bf16":
+        out = out.bfloat16().float()
+    return out
+
+
+def drift_stack(wname: str, device, layers: int = 32, full_layers=(7, 15, 23, 31), seed: int = 7,
+                reference: str = "cpu") -> dict:
     """Relative drift of a stack of attention layers run through the fused op
-    in bf16, against the same stack in fp32 on the CPU (the oracle).
+    in bf16, against the same stack in fp32 (BASELINE config 2's 32-layer
+    stack; the reference's precision caveat is its README.md:10).
 
     Layer l normalises each token of ``x_l [N, H, D]`` to unit RMS (a
     pre-norm block, which keeps the logits O(1) however far the residual
@@ -355,16 +439,17 @@ def drift_stack(wname: str, device, layers: int = 32, full_layers=(7, 15, 23, 31
     ``x_{l+1} = x_l + attn_l(q, k, v)``.  Window layers use the workload's
     window ``cu_seqlens``; layers in ``full_layers`` attend over the whole
     image (the tokens stay in window order, as in the Qwen2.5-VL encoder).
-    The GPU stack keeps activations in bf16.  A third stack runs the oracle's
-    bf16 rounding model on the CPU: the drift any bf16 pipeline with these
-    rounding points has, i.e. the floor the GPU stack is compared with.
+    The GPU stack keeps activations in bf16.  A third stack runs the bf16
+    rounding model (the same rounding points evaluated exactly): the drift
+    any bf16 pipeline with these rounding points has, i.e. the floor the GPU
+    stack is compared with.  The two reference stacks run in the numpy
+    oracle on the CPU (``reference="cpu"``) or in plain torch float32 on the
+    GPU (``reference="gpu"``, ``torch_reference_attention``) for sizes where
+    the CPU model of the rounding takes minutes per layer.
     Returns per-layer ``||x - x_ref|| / ||x_ref||`` of both."""
     import math
 
     import numpy as np
-
-    from oracle import attention as A
-    from oracle.numerics import round_bf16
 
     w = WORKLOADS[wname]
     inp = make_inputs(w, seed=seed, device="cpu", heads=1)
@@ -373,29 +458,46 @@ def drift_stack(wname: str, device, layers: int = 32, full_layers=(7, 15, 23, 31
     cu_full = torch.tensor([0, n], dtype=torch.int32)
     g = torch.Generator().manual_seed(seed)
     x0 = torch.randn(n, h, d, generator=g)
-    cos_np, sin_np = cos.float().numpy(), sin.float().numpy()
     cos_d, sin_d = cos.to(device), sin.to(device)
-    xr = x0.numpy().copy()
-    xe = round_bf16(xr)
+    if reference == "cpu":
+        from oracle import attention as A
+        from oracle.numerics import round_bf16
+        cos_np, sin_np = cos.float().numpy(), sin.float().numpy()
+        xr = x0.numpy().copy()
+        xe = round_bf16(xr)
+    else:
+        xr = x0.to(device)
+        xe = xr.bfloat16().float()
     xg = x0.to(torch.bfloat16).to(device)
+    scale = d ** -0.5
     rows = []
     for layer in range(layers):
         wts = torch.randn(3, h, d, d, generator=g) / math.sqrt(d)
         full = layer in full_layers
         cu = cu_full if full else cu_win
-        cu_np = cu.numpy()
         ms = int((cu[1:] - cu[:-1]).max())
-        wn = wts.numpy()
-        def rms(x):
-            return x / np.sqrt(np.mean(np.square(x), axis=(1, 2), keepdims=True) + np.float32(1e-6))
+        if reference == "cpu":
+            cu_np, wn = cu.numpy(), wts.numpy()
 
-        # fp32 reference
-        qkv = np.matmul(rms(xr).transpose(1, 0, 2)[None], wn).transpose(0, 2, 1, 3)
-        xr = xr + A.fused_rope_attention(qkv[0], qkv[1], qkv[2], cos_np, sin_np, cu_np, mode="fp32")
-        # bf16 rounding model
-        qkv = round_bf16(np.matmul(rms(xe).transpose(1, 0, 2)[None], wn).transpose(0, 2, 1, 3))
-        att = A.fused_rope_attention(qkv[0], qkv[1], qkv[2], cos_np, sin_np, cu_np, mode="bf16")
-        xe = round_bf16(xe + att)
+            def rms(x):
+                return x / np.sqrt(np.mean(np.square(x), axis=(1, 2), keepdims=True) + np.float32(1e-6))
+
+            qkv = np.matmul(rms(xr).transpose(1, 0, 2)[None], wn).transpose(0, 2, 1, 3)
+            xr = xr + A.fused_rope_attention(qkv[0], qkv[1], qkv[2], cos_np, sin_np, cu_np, mode="fp32")
+            qkv = round_bf16(np.matmul(rms(xe).transpose(1, 0, 2)[None], wn).transpose(0, 2, 1, 3))
+            att = A.fused_rope_attention(qkv[0], qkv[1], qkv[2], cos_np, sin_np, cu_np, mode="bf16")
+            xe = round_bf16(xe + att)
+        else:
+            wd, cud = wts.to(device), cu.to(device)
+
+            def rms_t(x):
+                return x * torch.rsqrt(x.square().mean(dim=(1, 2), keepdim=True) + 1e-6)
+
+            qkv = torch.matmul(rms_t(xr).transpose(0, 1)[None], wd).transpose(1, 2)
+            xr = xr + torch_reference_attention(qkv[0], qkv[1], qkv[2], cos_d.float(), sin_d.float(), cud, scale)
+            qkv = torch.matmul(rms_t(xe).transpose(0, 1)[None], wd).transpose(1, 2).bfloat16().float()
+            att = torch_reference_attention(qkv[0], qkv[1], qkv[2], cos_d.float(), sin_d.float(), cud, scale, "bf16")
+            xe = (xe + att).bfloat16().float()
         # the fused op on the GPU (projections in fp32, activations stored in bf16)
         xf = xg.float()
         xf = xf * torch.rsqrt(xf.square().mean(dim=(1, 2), keepdim=True) + 1e-6)
@@ -403,14 +505,19 @@ def drift_stack(wname: str, device, layers: int = 32, full_layers=(7, 15, 23, 31
         qkv = qkv.to(torch.bfloat16).contiguous()
         out = fused_rope_attention(qkv[0], qkv[1], qkv[2], cos_d, sin_d, cu.to(device), ms)
         xg = (xg.float() + out.float()).to(torch.bfloat16)
-        ref_norm = float(np.linalg.norm(xr))
-        gpu = float(np.linalg.norm(xg.float().cpu().numpy() - xr)) / ref_norm
-        emu = float(np.linalg.norm(xe - xr)) / ref_norm
+        if reference == "cpu":
+            ref_norm = float(np.linalg.norm(xr))
+            gpu = float(np.linalg.norm(xg.float().cpu().numpy() - xr)) / ref_norm
+            emu = float(np.linalg.norm(xe - xr)) / ref_norm
+        else:
+            ref_norm = float(torch.linalg.vector_norm(xr))
+            gpu = float(torch.linalg.vector_norm(xg.float() - xr)) / ref_norm
+            emu = float(torch.linalg.vector_norm(xe - xr)) / ref_norm
         rows.append({"layer": layer, "kind": "full" if full else "window", "gpu_rel": gpu, "bf16_model_rel": emu})
         print(f"[drift] layer {layer:2d} {'full  ' if full else 'window'} gpu {gpu:.3e}  bf16-model {emu:.3e}",
               file=sys.stderr, flush=True)
     return {"workload": wname, "layers": layers, "full_layers": list(full_layers), "tokens": n, "heads": h,
-            "head_dim": d, "per_layer": rows, "final_gpu_rel": rows[-1]["gpu_rel"],
+            "head_dim": d, "reference": reference, "per_layer": rows, "final_gpu_rel": rows[-1]["gpu_rel"],
             "final_bf16_model_rel": rows[-1]["bf16_model_rel"]}
 
 
@@ -433,6 +540,9 @@ def main() -> int:
                          "workload and write them to FILE")
     ap.add_argument("--backward", default=None, metavar="FILE",
                     help="measure the backward of every workload and write them to FILE")
+    ap.add_argument("--floor", action="store_true",
+                    help="time the floor probe (one elementwise kernel reading q, k, v and writing an output) on "
+                         "--workload's tensors instead of the op (also a --profile-calls driver option)")
     ap.add_argument("--drift", default=None, metavar="FILE",
                     help="run the 32-layer drift stack on --workload's grid and write the report to FILE")
     args = ap.parse_args()
@@ -469,8 +579,20 @@ def main() -> int:
         with open(args.backward, "w") as f:
             json.dump(rows, f, indent=1)
         return 0
+    if args.floor:
+        w = WORKLOADS[args.workload]
+        inp = make_inputs(w, seed=1234 + list(WORKLOADS).index(args.workload), device=dev)
+        m = time_calls(floor_call(inp), args.steps, args.warmup, flush)
+        nbytes = 4 * inp["q"].numel() * inp["q"].element_size()
+        print(json.dumps({"floor": args.workload, "kernel": "torch.addcmul(q, k, v)", "bytes": nbytes,
+                          **{k: round(v, 3) for k, v in m.items()},
+                          "cold_GBps": round(nbytes / (m["cold_median_us"] * 1e-6) / 1e9, 1),
+                          "warm_GBps": round(nbytes / (m["warm_us"] * 1e-6) / 1e9, 1),
+                          "cold_frac_of_8TBps": round(nbytes / (m["cold_median_us"] * 1e-6) / 8e12, 4)}),
+              flush=True)
+        return 0
     if args.drift:
-        rep = drift_stack(args.workload, dev)
+        rep = drift_stack(args.workload, dev, reference="gpu")
         with open(args.drift, "w") as f:
             json.dump(rep, f, indent=1)
         print(json.dumps({"drift": args.workload, "final_gpu_rel": rep["final_gpu_rel"],

@@ -105,6 +105,7 @@ SIGNATURES = {
     "fra_sizeof_args": (ctypes.c_int32, []),
     "fra_sizeof_plan": (ctypes.c_int32, []),
     "fra_bwd_varlen": (ctypes.c_int, [ctypes.POINTER(BwdArgs), ctypes.c_void_p]),
+    "fra_bwd_query_plan": (ctypes.c_int, [ctypes.POINTER(BwdArgs), ctypes.POINTER(Plan)]),
     "fra_bwd_workspace_bytes": (ctypes.c_int, [ctypes.POINTER(BwdArgs), ctypes.POINTER(ctypes.c_int64)]),
     "fra_sizeof_bwd_args": (ctypes.c_int32, []),
 }

@@ -3,8 +3,21 @@
 Usage: ``python -m fused_rope_attn_amd.build`` (or ``build()`` from Python).
 The library lands next to this file, where ``_lib.py`` loads it from, so it
 travels with the source tree.  Building needs hipcc but no GPU.
+
+Translation units, compiled in parallel:
+
+* ``fra_fwd.hip`` and ``fra_bwd.hip`` -- argument checks, kernel choice and
+  the C ABI (no kernels);
+* ``fra_inst.hip`` once per head_dim of ``FRA_HEAD_DIMS``
+  (``csrc/fra_fwd_types.h``), with ``-DFRA_HEAD_DIM=<D>``: that head_dim's
+  forward and backward kernels.
+
+``FRA_BUILD_DIMS=80,72`` (environment) builds only those head dims, for
+quicker iteration on a kernel; the library then reports every other head_dim
+as unsupported.  The default builds all.
 """
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -13,9 +26,6 @@ import tempfile
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
-# Forward (fra_kernels.hip: kernels, dispatch and most of the C ABI) and
-# backward (fra_bwd.hip) translation units, compiled in parallel.
-SRCS = [os.path.join(CSRC, "fra_kernels.hip"), os.path.join(CSRC, "fra_bwd.hip")]
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libfra.so")
 ARCH = "gfx950"
@@ -28,7 +38,19 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; set HIPCC or install ROCm")
 
 
-def compile_command(src: str, obj: str) -> list:
+def head_dims() -> list:
+    """The head dims of FRA_HEAD_DIMS in csrc/fra_fwd_types.h (or FRA_BUILD_DIMS)."""
+    env = os.environ.get("FRA_BUILD_DIMS", "").strip()
+    if env:
+        return [int(x) for x in env.split(",") if x.strip()]
+    with open(os.path.join(CSRC, "fra_fwd_types.h")) as f:
+        m = re.search(r"#define FRA_HEAD_DIMS\(X\)\s+(.*)", f.read())
+    if not m:
+        raise RuntimeError("FRA_HEAD_DIMS not found in fra_fwd_types.h")
+    return [int(x) for x in re.findall(r"X\((\d+)\)", m.group(1))]
+
+
+def compile_command(src: str, obj: str, defines=()) -> list:
     return [
         hipcc(),
         f"--offload-arch={ARCH}",
@@ -41,6 +63,7 @@ def compile_command(src: str, obj: str) -> list:
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-I", INCLUDE,
         "-I", CSRC,
+        *defines,
         "-o", obj,
         src,
     ]
@@ -54,20 +77,37 @@ def _clean(stderr: str) -> str:
     return "\n".join(l for l in stderr.splitlines() if "packed-fp32-ops" not in l)
 
 
+def units(tmpd: str) -> list:
+    """(source, object, defines) of every translation unit."""
+    dims = head_dims()
+    common = []
+    if os.environ.get("FRA_BUILD_DIMS", "").strip():
+        common = ["-DFRA_HEAD_DIMS(X)=" + " ".join(f"X({d})" for d in dims)]
+    out = [(os.path.join(CSRC, s), os.path.join(tmpd, s + ".o"), common) for s in ("fra_fwd.hip", "fra_bwd.hip")]
+    for d in dims:
+        out.append((os.path.join(CSRC, "fra_inst.hip"), os.path.join(tmpd, f"fra_inst_d{d}.o"),
+                    common + [f"-DFRA_HEAD_DIM={d}"]))
+    return out
+
+
 def build(verbose: bool = False) -> str:
     """Compile the library; returns its path.  Always recompiles."""
+    jobs = max(1, min(16, os.cpu_count() or 1))
     with tempfile.TemporaryDirectory(prefix="fra_build_") as tmpd:
-        objs = [os.path.join(tmpd, os.path.basename(s) + ".o") for s in SRCS]
-        cmds = [compile_command(s, o) for s, o in zip(SRCS, objs)]
+        todo = [(compile_command(s, o, dfs), o) for s, o, dfs in units(tmpd)]
+        objs = [o for _, o in todo]
         if verbose:
-            for c in cmds:
+            for c, _ in todo:
                 print(" ".join(c), flush=True)
-        procs = [subprocess.Popen(c, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True) for c in cmds]
-        errs = []
-        for c, pr in zip(cmds, procs):
+        errs, running = [], []
+        while todo or running:
+            while todo and len(running) < jobs:
+                c, _ = todo.pop(0)
+                running.append((c, subprocess.Popen(c, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+            c, pr = running.pop(0)
             _, err = pr.communicate()
             if pr.returncode != 0:
-                errs.append(f"hipcc failed ({pr.returncode}) on {c[-1]}:\n{_clean(err)}")
+                errs.append(f"hipcc failed ({pr.returncode}) on {' '.join(c[-3:])}:\n{_clean(err)}")
             elif verbose and _clean(err).strip():
                 print(_clean(err), file=sys.stderr)
         if errs:

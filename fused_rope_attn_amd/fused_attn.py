@@ -24,7 +24,7 @@ import torch
 from . import _lib
 
 __all__ = ["fused_rope_attention", "fused_rope_attention_fwd", "fused_rope_attention_bwd",
-           "compute_rope_2d", "next_pow2", "plan"]
+           "compute_rope_2d", "next_pow2", "plan", "backward_plan"]
 
 
 def next_pow2(n: int) -> int:
@@ -171,6 +171,9 @@ def _validate(q, k, v, cos, sin, cu_seqlens, out) -> None:
     total_seq, num_heads, head_dim = (int(q.shape[0]), int(q.shape[1]), int(q.shape[2]))
     if head_dim <= 0 or head_dim % 2 != 0:
         raise ValueError(f"head_dim must be positive and even, got {head_dim}")
+    if head_dim > MAX_HEAD_DIM:
+        raise ValueError(f"head_dim must be <= {MAX_HEAD_DIM} (the kernels keep a query row's rotated "
+                         f"head_dim values in registers), got {head_dim}")
     widths = ((total_seq, head_dim // 2), (total_seq, head_dim))
     if tuple(cos.shape) not in widths or tuple(sin.shape) != tuple(cos.shape):
         raise ValueError(
@@ -194,6 +197,62 @@ def _validate(q, k, v, cos, sin, cu_seqlens, out) -> None:
     for name, t in (("k", k), ("v", v), ("cos", cos), ("sin", sin)):
         if t.device != q.device:
             raise ValueError(f"{name} must be on {q.device}, got {t.device}")
+
+
+# ---------------------------------------------------------------------------
+# head_dim coverage.  The reference takes any even head_dim and pads it to a
+# power of two inside its kernel (fused_attn.py:167-168, 215-216).  Here the
+# library has kernels for a fixed set of head dims (fra_supports_head_dim);
+# any other even head_dim up to MAX_HEAD_DIM runs at the next compiled one
+# with zero-padded inputs, which changes no result: the padded dims add 0 to
+# every dot product and the padded value columns are dropped.
+# ---------------------------------------------------------------------------
+
+MAX_HEAD_DIM = 128
+
+_kernel_dims: "dict[int, int]" = {}
+
+
+def _kernel_head_dim(d: int) -> int:
+    """The head_dim the kernels run ``d`` at (``d`` itself when compiled)."""
+    dp = _kernel_dims.get(d)
+    if dp is None:
+        if d > MAX_HEAD_DIM:
+            raise ValueError(f"head_dim must be <= {MAX_HEAD_DIM} (the kernels keep a query row's rotated "
+                             f"head_dim values in registers), got {d}")
+        lib = _lib.load()
+        dp = next((c for c in range(d, MAX_HEAD_DIM + 1) if c % 8 == 0 and lib.fra_supports_head_dim(c)), None)
+        if dp is None:
+            raise ValueError(f"head_dim={d} has no kernel at or above it in this build of libfra.so")
+        _kernel_dims[d] = dp
+    return dp
+
+
+def _pad_halves(x: torch.Tensor, d: int, dp: int) -> torch.Tensor:
+    """``[..., d]`` -> ``[..., dp]`` keeping the rotation's split-half pairs:
+    ``x[..., :d/2]`` at ``[0, d/2)`` and ``x[..., d/2:]`` at
+    ``[dp/2, dp/2 + d/2)``; zeros elsewhere."""
+    y = x.new_zeros(*x.shape[:-1], dp)
+    y[..., : d // 2] = x[..., : d // 2]
+    y[..., dp // 2: dp // 2 + d // 2] = x[..., d // 2:]
+    return y
+
+
+def _unpad_halves(y: torch.Tensor, d: int, dp: int) -> torch.Tensor:
+    return torch.cat([y[..., : d // 2], y[..., dp // 2: dp // 2 + d // 2]], dim=-1)
+
+
+def _pad_tail(x: torch.Tensor, d: int, dp: int) -> torch.Tensor:
+    """``[..., d]`` -> ``[..., dp]`` with zeros after the first d values."""
+    y = x.new_zeros(*x.shape[:-1], dp)
+    y[..., :d] = x
+    return y
+
+
+def _pad_table(t: torch.Tensor, d: int, dp: int) -> torch.Tensor:
+    """cos/sin of width d/2 -> dp/2 (zeros after), width d -> dp (halves
+    split as in ``_pad_halves``)."""
+    return _pad_tail(t, d // 2, dp // 2) if t.shape[-1] == d // 2 else _pad_halves(t, d, dp)
 
 
 def _uses_long_kernel(max_seqlen: int, head_dim: int) -> bool:
@@ -243,7 +302,14 @@ def _workspace_bytes(lib, args) -> int:
 def plan(q, k, v, cos, sin, cu_seqlens, max_seqlen: int, softmax_scale=None) -> dict:
     """Which kernel ``fused_rope_attention`` launches for these inputs
     (no launch): ``{"kernel", "name", "grid", "block", "block_q",
-    "block_kv", "lds_bytes"}``."""
+    "block_kv", "lds_bytes", ...}``; for a head_dim without kernels of its
+    own, the plan of the zero-padded call that runs instead."""
+    d = q.shape[2]
+    dp = _kernel_head_dim(d)
+    if dp != d:
+        scale = d ** -0.5 if softmax_scale is None else softmax_scale
+        return plan(_pad_halves(q, d, dp), _pad_halves(k, d, dp), _pad_tail(v, d, dp), _pad_table(cos, d, dp),
+                    _pad_table(sin, d, dp), cu_seqlens, max_seqlen, scale)
     cu = _prepare_cu(cu_seqlens, q.device)
     q2, k2, v2, cos2, sin2 = _prepare(q, k, v, cos, sin, _uses_long_kernel(int(max_seqlen), q.shape[2]))
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -314,6 +380,15 @@ def _forward(q, k, v, cos, sin, cu, max_seqlen: int, scale: float, out, lse):
         if lse is not None:
             lse.fill_(float("-inf"))
         return out.zero_()
+    d = q.shape[2]
+    dp = _kernel_head_dim(d)
+    if dp != d:
+        # The padded output starts as a copy of ``out`` so that rows outside
+        # every segment come back unchanged.
+        outp = _pad_tail(out, d, dp)
+        _forward(_pad_halves(q, d, dp), _pad_halves(k, d, dp), _pad_tail(v, d, dp), _pad_table(cos, d, dp),
+                 _pad_table(sin, d, dp), cu, max_seqlen, scale, outp, lse)
+        return out.copy_(outp[..., :d])
     qk, kk, vk, cosk, sink = _prepare(q, k, v, cos, sin, _uses_long_kernel(max_seqlen, q.shape[2]))
     dst = out if _fits(out, 8, 4) else torch.empty(q.shape, dtype=q.dtype, device=q.device)
 
@@ -363,20 +438,16 @@ def _bwd_layout(t: torch.Tensor) -> torch.Tensor:
     return _kernel_layout(t, 16, 8)
 
 
-def _backward(dout, q, k, v, cos, sin, out, lse, cu, max_seqlen: int, scale: float, dq, dk, dv):
-    """One backward launch (``fra_bwd_varlen``) writing dq, dk, dv."""
-    if max_seqlen <= 0 or q.shape[0] == 0:
-        return dq, dk, dv
-    lib = _lib.load()
+def _bwd_args(dout, q, k, v, cos, sin, out, lse, cu, max_seqlen: int, scale: float, dq, dk, dv):
+    """``fra_bwd_args`` of one backward call, and the tensors it points to
+    (kept alive by the caller until the launch)."""
     q2, k2, v2, o2, do2 = (_bwd_layout(t) for t in (q, k, v, out, dout))
     # The backward reads float32 tables (widening is exact).
     cos2 = cos.float().contiguous()
     sin2 = sin.float().contiguous()
     lse2 = lse.contiguous()
-    dsts = [t if _fits(t, 16, 8) else torch.empty(q.shape, dtype=q.dtype, device=q.device) for t in (dq, dk, dv)]
     a = _lib.BwdArgs()
-    for name, t in (("q", q2), ("k", k2), ("v", v2), ("out", o2), ("dout", do2),
-                    ("dq", dsts[0]), ("dk", dsts[1]), ("dv", dsts[2])):
+    for name, t in (("q", q2), ("k", k2), ("v", v2), ("out", o2), ("dout", do2), ("dq", dq), ("dk", dk), ("dv", dv)):
         setattr(a, name, t.data_ptr())
         setattr(a, f"{name}_stride_seq", t.stride(0))
         setattr(a, f"{name}_stride_head", t.stride(1))
@@ -390,6 +461,46 @@ def _backward(dout, q, k, v, cos, sin, out, lse, cu, max_seqlen: int, scale: flo
     a.rope_dtype = _lib.FRA_DTYPE_F32
     a.softmax_scale = float(scale)
     a.flags = 0
+    return a, (q2, k2, v2, o2, do2, cos2, sin2, lse2)
+
+
+def backward_plan(q, k, v, cos, sin, cu_seqlens, max_seqlen: int) -> dict:
+    """Which main kernel the backward of these inputs launches (no launch):
+    ``{"kernel", "name", "grid", "block"}``; for a head_dim without kernels
+    of its own, the plan of the zero-padded call that runs instead."""
+    d = q.shape[2]
+    dp = _kernel_head_dim(d)
+    if dp != d:
+        return backward_plan(_pad_halves(q, d, dp), _pad_halves(k, d, dp), _pad_tail(v, d, dp),
+                             _pad_table(cos, d, dp), _pad_table(sin, d, dp), cu_seqlens, max_seqlen)
+    cu = _prepare_cu(cu_seqlens, q.device)
+    z = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
+    a, _keep = _bwd_args(z, q, k, v, cos, sin, z, lse, cu, max_seqlen, q.shape[2] ** -0.5, z, z, z)
+    pl = _lib.Plan()
+    _lib.check(_lib.load().fra_bwd_query_plan(a, pl))
+    return {"kernel": {_lib.FRA_KERNEL_WINDOW: "window", _lib.FRA_KERNEL_LONG: "long"}.get(pl.kernel, "none"),
+            "name": pl.name.decode(), "grid": pl.grid, "block": pl.block}
+
+
+def _backward(dout, q, k, v, cos, sin, out, lse, cu, max_seqlen: int, scale: float, dq, dk, dv):
+    """One backward launch (``fra_bwd_varlen``) writing dq, dk, dv."""
+    if max_seqlen <= 0 or q.shape[0] == 0:
+        return dq, dk, dv
+    d = q.shape[2]
+    dp = _kernel_head_dim(d)
+    if dp != d:
+        dqp, dkp, dvp = _pad_halves(dq, d, dp), _pad_halves(dk, d, dp), _pad_tail(dv, d, dp)
+        _backward(_pad_tail(dout, d, dp), _pad_halves(q, d, dp), _pad_halves(k, d, dp), _pad_tail(v, d, dp),
+                  _pad_table(cos, d, dp), _pad_table(sin, d, dp), _pad_tail(out, d, dp), lse, cu, max_seqlen,
+                  scale, dqp, dkp, dvp)
+        dq.copy_(_unpad_halves(dqp, d, dp))
+        dk.copy_(_unpad_halves(dkp, d, dp))
+        dv.copy_(dvp[..., :d])
+        return dq, dk, dv
+    lib = _lib.load()
+    dsts = [t if _fits(t, 16, 8) else torch.empty(q.shape, dtype=q.dtype, device=q.device) for t in (dq, dk, dv)]
+    a, _keep = _bwd_args(dout, q, k, v, cos, sin, out, lse, cu, max_seqlen, scale, *dsts)
     with torch.cuda.device(q.device):
         nbytes = ctypes.c_int64(0)
         _lib.check(lib.fra_bwd_workspace_bytes(a, ctypes.byref(nbytes)))

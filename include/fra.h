@@ -223,6 +223,13 @@ int fra_bwd_varlen(const fra_bwd_args *args, void *stream);
 /* Workspace bytes fra_bwd_varlen() needs for these arguments. */
 int fra_bwd_workspace_bytes(const fra_bwd_args *args, int64_t *bytes);
 
+/* Fill *plan with the backward's main kernel for args without launching
+ * anything: kernel FRA_KERNEL_WINDOW (one workgroup per (segment, head);
+ * name "bwd_window_..." or, with V held in registers, "bwd_window_vreg_...")
+ * or FRA_KERNEL_LONG ("bwd_long_...", the dq and dk/dv units); grid and
+ * block of that kernel.  No counterpart in the reference (forward-only). */
+int fra_bwd_query_plan(const fra_bwd_args *args, fra_plan *plan);
+
 /* 1 if head_dim has a compiled kernel in this build, else 0. */
 int fra_supports_head_dim(int32_t head_dim);
 

@@ -9,8 +9,8 @@ Contents (each function cites the reference file:line it restates):
 
 * ``numerics``  -- bf16 / fp16 round-to-nearest-even emulation in numpy.
 * ``rope``      -- ``compute_rope_2d`` (reference ``fused_attn.py:33-136``).
-* ``windows``   -- ``get_window_index`` / ``window_shuffle`` /
-  ``window_unshuffle`` (reference ``utils.py:12-153``).
+* ``windows``   -- ``get_window_index`` (reference ``utils.py:12-102``) and
+  the per-frame ``cu_seqlens`` of full-attention layers.
 * ``attention`` -- the unfused path: split-half rotation
   (``fused_attn.py:340-345,385-390``) followed by per-segment non-causal
   softmax attention (``fused_attn.py:347-423``), in fp32 (the official

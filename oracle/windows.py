@@ -15,8 +15,10 @@ Restates ``get_window_index`` (reference ``utils.py:12-102``):
 * ``cu_seqlens`` is the cumulative window size times ``merge**2``
   (``:92-93``) with repeated entries removed (``:100-102``).
 
-``window_shuffle`` / ``window_unshuffle`` gather over merge units
-(``utils.py:105-153``).
+The window (un)shuffle of ``utils.py:105-153`` is a plain gather; the
+product's copy (``fused_rope_attn_amd/utils.py``) is checked directly against
+the Hugging Face encoder's reorder of its rotary tables
+(``tests/test_golden.py``), so the oracle carries none.
 """
 import numpy as np
 
@@ -65,18 +67,3 @@ def full_cu_seqlens(grid_thw, per_frame: bool = True):
             cu.append(cu[-1] + t * h * w)
     return np.asarray(cu, dtype=np.int32)
 
-
-def window_shuffle(x: np.ndarray, widx: np.ndarray, spatial_merge_size: int = 2):
-    """Gather tokens into window order over merge units (utils.py:105-126)."""
-    mu = spatial_merge_size ** 2
-    n = x.shape[0] // mu
-    return x.reshape(n, mu, *x.shape[1:])[widx].reshape(x.shape)
-
-
-def window_unshuffle(x: np.ndarray, widx: np.ndarray, spatial_merge_size: int = 2):
-    """Inverse of ``window_shuffle`` (utils.py:129-153)."""
-    mu = spatial_merge_size ** 2
-    n = x.shape[0] // mu
-    inv = np.empty_like(widx)
-    inv[widx] = np.arange(n, dtype=widx.dtype)
-    return x.reshape(n, mu, *x.shape[1:])[inv].reshape(x.shape)

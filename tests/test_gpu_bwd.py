@@ -25,7 +25,7 @@ import numpy as np
 import pytest
 import torch
 
-from fused_rope_attn_amd import fused_rope_attention, fused_rope_attention_bwd, fused_rope_attention_fwd
+from fused_rope_attn_amd import backward_plan, fused_rope_attention, fused_rope_attention_bwd, fused_rope_attention_fwd
 from oracle import attention as A
 
 pytestmark = pytest.mark.gpu
@@ -84,7 +84,7 @@ def check_lse(got, ref, what):
 
 
 CASES = [
-    # (lens, heads, head_dim, width, dtype, lead_rows, extra_rows)
+    # (lens, heads, head_dim, width, dtype, lead_rows, extra_rows[, backward kernel on 256 CUs])
     ([64, 64, 40, 1], 2, 80, None, torch.bfloat16, 0, 0),      # window kernels (2 waves)
     ([64, 0, 17, 64], 3, 72, None, torch.bfloat16, 2, 3),      # window, empty segment, uncovered rows
     ([33, 64], 2, 64, 64, torch.float16, 0, 1),               # window, full-width tables, fp16
@@ -95,18 +95,30 @@ CASES = [
     ([1000], 1, 80, None, torch.bfloat16, 0, 0),              # long, many key/query blocks
     # window grids of 768 < segments x heads <= 1024 (256 CUs): the variant
     # with V in registers, four workgroups per CU
-    ([64] * 52 + [17, 0, 5, 33], 16, 80, None, torch.bfloat16, 0, 0),
-    ([64] * 58 + [40, 2], 16, 72, 72, torch.float16, 0, 2),
-    ([64] * 49 + [1], 16, 64, None, torch.bfloat16, 3, 0),
+    ([64] * 52 + [17, 0, 5, 33], 16, 80, None, torch.bfloat16, 0, 0, "bwd_window_vreg"),
+    ([64] * 58 + [40, 2], 16, 72, 72, torch.float16, 0, 2, "bwd_window_vreg"),
+    ([64] * 49 + [1], 16, 64, None, torch.bfloat16, 3, 0, "bwd_window_vreg"),
+    # head_dim 96 window backward: half-width tables with the register-V
+    # instance (grid in (3, 4] x CUs) and the staged one (below it); full
+    # width (no register-V instance); head_dim 128 (the forward sends it to
+    # the long kernel, the backward to the window kernel)
+    ([64] * 60 + [33, 5], 13, 96, None, torch.bfloat16, 0, 1, "bwd_window_vreg"),
+    ([64, 64, 21, 0, 64], 3, 96, None, torch.bfloat16, 1, 0, "bwd_window_d"),
+    ([64, 9, 64], 2, 96, 96, torch.float16, 0, 0, "bwd_window_d"),
+    ([64, 33, 64], 2, 128, None, torch.float16, 0, 2, "bwd_window_d"),
 ]
 
 
 @pytest.mark.parametrize("ci", range(len(CASES)))
 def test_lse_and_backward_match_oracle(device, ci):
-    lens, h, d, width, dtype, lead, extra = CASES[ci]
+    lens, h, d, width, dtype, lead, extra = CASES[ci][:7]
     case = make_case(lens, h, d, seed=500 + ci, dtype=dtype, width=width, lead_rows=lead, extra_rows=extra)
     print(f"case {ci}: lens={lens} h={h} d={d} width={width} dtype={dtype}", flush=True)
-    out, lse, dq, dk, dv = gpu_fwd_bwd(on(case, device))
+    c = on(case, device)
+    if len(CASES[ci]) > 7 and torch.cuda.get_device_properties(device).multi_processor_count == 256:
+        name = backward_plan(c["q"], c["k"], c["v"], c["cos"], c["sin"], c["cu"], c["max_seqlen"])["name"]
+        assert name.startswith(CASES[ci][7]), (name, CASES[ci][7])
+    out, lse, dq, dk, dv = gpu_fwd_bwd(c)
     q, k, v, do = (f32(case[x]) for x in ("q", "k", "v", "dout"))
     cos, sin, cu = f32(case["cos"]), f32(case["sin"]), case["cu"].numpy()
     ref_lse = A.softmax_lse(q, k, cos, sin, cu)
