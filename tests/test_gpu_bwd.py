@@ -9,8 +9,11 @@ are the target.  Tolerances, all against the fp32 oracle:
 * lse (natural log, values ~5-8): max-abs <= 1e-2, mean-abs <= 1e-3.  The
   bf16 rounding of q_rot / k_rot alone moves it by up to 1.6e-3 (mean 4e-4)
   in the rounding-point model (oracle mode "bf16").
-* dq, dk, dv in bf16 (magnitudes <= ~1.5): max-abs <= 2e-2 and mean-abs <=
-  2e-3 (the forward's north-star bounds), and mean-abs <= 1e-2 x mean |ref|.
+* dq, dk, dv in bf16 (magnitudes <= ~1.5 at head_dim 80, growing with
+  head_dim): max-abs <= max(2e-2, 5e-3 x max |ref|) -- the forward's
+  north-star bound, or about two bf16 rounding steps of the largest gradient
+  (storing a value x in bf16 alone errs by up to x * 2^-9) -- and mean-abs <=
+  2e-3 and <= 1e-2 x mean |ref|.
   The rounding-point model of the kernels (q_rot/k_rot, P, dZ and the
   results rounded to bf16) sits at 3-4e-3 x mean |ref| and <= 1e-2 x max |ref|.
 
@@ -31,7 +34,7 @@ from oracle import attention as A
 pytestmark = pytest.mark.gpu
 
 LSE_MAX, LSE_MEAN = 1e-2, 1e-3
-G_MAX, G_MEAN, G_REL_MEAN = 2e-2, 2e-3, 1e-2
+G_MAX, G_MEAN, G_REL_MEAN, G_REL_MAX = 2e-2, 2e-3, 1e-2, 5e-3
 
 
 def f32(t):
@@ -69,8 +72,9 @@ def check_grad(got, ref, what):
     err = np.abs(got[covered] - ref[covered])
     assert np.isfinite(got[covered]).all(), f"{what}: non-finite gradient"
     mx, mn, rm = float(err.max()), float(err.mean()), float(np.abs(ref[covered]).mean())
-    assert mx <= G_MAX and mn <= G_MEAN and mn <= G_REL_MEAN * rm, (
-        f"{what}: max-abs {mx:.3e} (<= {G_MAX}), mean-abs {mn:.3e} (<= {G_MEAN} and <= {G_REL_MEAN} x {rm:.3e})")
+    bound = max(G_MAX, G_REL_MAX * float(np.abs(ref[covered]).max()))
+    assert mx <= bound and mn <= G_MEAN and mn <= G_REL_MEAN * rm, (
+        f"{what}: max-abs {mx:.3e} (<= {bound:.3e}), mean-abs {mn:.3e} (<= {G_MEAN} and <= {G_REL_MEAN} x {rm:.3e})")
     # rows outside every segment: zero (freshly allocated results)
     assert np.all(got[~covered] == 0), f"{what}: rows outside the segments were written"
 
