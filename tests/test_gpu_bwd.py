@@ -10,10 +10,11 @@ are the target.  Tolerances, all against the fp32 oracle:
   bf16 rounding of q_rot / k_rot alone moves it by up to 1.6e-3 (mean 4e-4)
   in the rounding-point model (oracle mode "bf16").
 * dq, dk, dv in bf16 (magnitudes <= ~1.5 at head_dim 80, growing with
-  head_dim): max-abs <= max(2e-2, 5e-3 x max |ref|) -- the forward's
-  north-star bound, or about two bf16 rounding steps of the largest gradient
-  (storing a value x in bf16 alone errs by up to x * 2^-9) -- and mean-abs <=
-  2e-3 and <= 1e-2 x mean |ref|.
+  head_dim): max-abs <= max(2e-2, 1e-2 x max |ref|) -- the forward's
+  north-star bound, or the rounding-point model's own worst case below
+  (storing a value x in bf16 alone errs by up to x * 2^-9; at head_dim 126
+  the largest dk is ~4.4 and errs by ~0.73% of it) -- and mean-abs <= 2e-3
+  and <= 1e-2 x mean |ref|.
   The rounding-point model of the kernels (q_rot/k_rot, P, dZ and the
   results rounded to bf16) sits at 3-4e-3 x mean |ref| and <= 1e-2 x max |ref|.
 
@@ -34,7 +35,7 @@ from oracle import attention as A
 pytestmark = pytest.mark.gpu
 
 LSE_MAX, LSE_MEAN = 1e-2, 1e-3
-G_MAX, G_MEAN, G_REL_MEAN, G_REL_MAX = 2e-2, 2e-3, 1e-2, 5e-3
+G_MAX, G_MEAN, G_REL_MEAN, G_REL_MAX = 2e-2, 2e-3, 1e-2, 1e-2
 
 
 def f32(t):
