@@ -96,6 +96,7 @@ class Plan(ctypes.Structure):
 # Every symbol include/fra.h declares, with its ctypes signature.
 SIGNATURES = {
     "fra_fwd_varlen": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.c_void_p]),
+    "fra_fwd_varlen_static": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.c_void_p]),
     "fra_query_plan": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(Plan)]),
     "fra_workspace_bytes": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(ctypes.c_int64)]),
     "fra_supports_head_dim": (ctypes.c_int, [ctypes.c_int32]),

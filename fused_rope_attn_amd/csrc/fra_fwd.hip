@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "fra.h"
 #include "fra_device.h"
@@ -88,7 +89,9 @@ const char *dtype_name(int dt) {
     }
 }
 
-int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
+// allow_pre false: the rotated-K part of a workspace is not used (K is
+// rotated in the long kernel); all of the workspace may hold split scratch.
+int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true) {
     if (!a) return fail(FRA_EINVAL, "args is NULL");
     if (a->flags != 0) return fail(FRA_EINVAL, "flags must be 0, got %d", a->flags);
     if (a->num_heads <= 0) return fail(FRA_EINVAL, "num_heads must be positive, got %d", a->num_heads);
@@ -220,7 +223,7 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp) {
         int64_t ws_left = a->workspace_bytes;
         kp.ws = (char *)a->workspace;
         c.pre = 0;
-        if (a->workspace && a->workspace_bytes >= kr_bytes && c.fn_pre) {
+        if (allow_pre && a->workspace && a->workspace_bytes >= kr_bytes && c.fn_pre) {
             c.pre = 1;
             c.fn = c.fn_pre;
             c.lds = c.lds_pre;
@@ -258,13 +261,10 @@ int fra_fail(int code, const char *fmt, ...) {
     return code;
 }
 
-extern "C" {
+namespace {
 
-int fra_fwd_varlen(const fra_fwd_args *args, void *stream) {
-    Choice c;
-    KParams kp;
-    const int rc = plan(args, c, kp);
-    if (rc != FRA_OK) return rc;
+// The launches of one planned forward call on `stream`.
+int launch(const fra_fwd_args *args, const Choice &c, const KParams &kp, void *stream) {
     g_err[0] = 0;
     if (args->total_seq == 0) return FRA_OK;
     if (c.split_parts > 1 && !args->workspace)
@@ -286,6 +286,81 @@ int fra_fwd_varlen(const fra_fwd_args *args, void *stream) {
         if (e != hipSuccess) return fail(FRA_EHIP, "launch of the merge of %s failed: %s", c.name, hipGetErrorString(e));
     }
     return FRA_OK;
+}
+
+// ---- the allocation-free entry point (fra_fwd_varlen_static) ----------------------
+//
+// Device scratch of fra_fwd_varlen_static(): the partial rows of a split last
+// round of the long kernel (per split unit and part, kLongBQ rows of
+// split_row_floats(head_dim) floats).  The split never gives more (unit,
+// part) pairs than the device has CUs, so with 256 CUs and head_dim <= 128
+// the largest need is 256 x 256 x 132 x 4 B = 34.6 MB.  Every device the
+// library runs on holds one copy until the process ends.  Nothing in it needs
+// to start at zero: each part writes every row the merge reads.
+constexpr int64_t kStaticScratchBytes = (int64_t)36 << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+
+// The current device's address of `scratch`, looked up once per device with
+// that device current (the array's name is only a host-side handle).
+int static_scratch(void **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(FRA_EHIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(FRA_EUNSUPPORTED, "device %d is beyond the %d the library tracks", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(FRA_EHIP, "hipGetSymbolAddress of the static scratch failed on device %d: %s", dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return FRA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fra_fwd_varlen(const fra_fwd_args *args, void *stream) {
+    Choice c;
+    KParams kp;
+    const int rc = plan(args, c, kp);
+    if (rc != FRA_OK) return rc;
+    return launch(args, c, kp, stream);
+}
+
+int fra_fwd_varlen_static(const fra_fwd_args *args, void *stream) {
+    if (!args) return fail(FRA_EINVAL, "args is NULL");
+    fra_fwd_args a = *args;
+    a.workspace = nullptr;
+    a.workspace_bytes = 0;
+    Choice c;
+    KParams kp;
+    int rc = plan(&a, c, kp, false);
+    if (rc != FRA_OK) return rc;
+    if (c.kernel == FRA_KERNEL_LONG) {
+        const SplitPlan sp = split_plan((int64_t)a.num_seqs * a.num_heads * kp.qblocks, a.max_seqlen, a.head_dim);
+        if (sp.parts > 1) {
+            if (sp.bytes > kStaticScratchBytes)
+                return fail(FRA_EUNSUPPORTED,
+                            "this call needs %lld bytes of scratch, more than the %lld bytes of the library's "
+                            "static scratch; use fra_fwd_varlen with a workspace",
+                            (long long)sp.bytes, (long long)kStaticScratchBytes);
+            rc = static_scratch(&a.workspace);
+            if (rc != FRA_OK) return rc;
+            a.workspace_bytes = sp.bytes;
+            rc = plan(&a, c, kp, false);
+            if (rc != FRA_OK) return rc;
+        }
+    }
+    return launch(&a, c, kp, stream);
 }
 
 int fra_workspace_bytes(const fra_fwd_args *args, int64_t *bytes) {

@@ -148,6 +148,21 @@ typedef struct fra_plan {
  */
 int fra_fwd_varlen(const fra_fwd_args *args, void *stream);
 
+/*
+ * fra_fwd_varlen() for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, semantics
+ * and outputs as fra_fwd_varlen() with args->workspace ignored: K is rotated
+ * inside the long kernel, and a split last round keeps its partial rows in a
+ * static device array of the library (36 MiB per device, held until the
+ * process ends; enough for any call on a device of up to 256 CUs at
+ * head_dim <= 128), so nothing is allocated or freed.  A call that would
+ * need more scratch than that returns FRA_EUNSUPPORTED.  Every call on one
+ * device shares that array: calls that overlap on one device (other streams,
+ * other threads) race and must be serialised by the caller.
+ */
+int fra_fwd_varlen_static(const fra_fwd_args *args, void *stream);
+
 /* Fill *plan with the kernel choice for args without launching anything
  * (the split fields reflect args->workspace_bytes). */
 int fra_query_plan(const fra_fwd_args *args, fra_plan *plan);
