@@ -1,6 +1,6 @@
 // fra_bwd.hip -- backward dispatch and its part of the C ABI (include/fra.h).
 // The kernels are in fra_bwd_kernels.h, compiled once per head_dim by
-// fra_inst.hip; see there for the arithmetic.
+// fra_inst_bwd.hip; see there for the arithmetic.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>

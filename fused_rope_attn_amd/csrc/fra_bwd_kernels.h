@@ -1,5 +1,5 @@
 // fra_bwd_kernels.h -- gfx950 backward kernels of the fused RoPE + varlen attention op.
-// Included by fra_inst.hip, which instantiates them for one head_dim.
+// Included by fra_inst_bwd.hip, which instantiates them for one head_dim.
 //
 // The reference is forward-only (fused_attn.py:139-423 has no autograd and
 // no softmax statistics output).  This file adds the training side of the

@@ -1,5 +1,5 @@
 // fra_bwd_types.h -- backward types shared by the dispatch (fra_bwd.hip) and
-// the per-head_dim kernel instances (fra_inst.hip).
+// the per-head_dim kernel instances (fra_inst_bwd.hip).
 #pragma once
 
 #include <stdint.h>
@@ -36,7 +36,7 @@ struct BwdKernels {
 };
 
 // Backward kernel instances of one head_dim (defined in fra_bwd_kernels.h,
-// instantiated by fra_inst.hip for every entry of FRA_HEAD_DIMS).
+// instantiated by fra_inst_bwd.hip for every entry of FRA_HEAD_DIMS).
 template <int D> BwdKernels bwd_kernels_d(int qkv, bool full);
 #define FRA_EXTERN_BWD_D(D) extern template BwdKernels bwd_kernels_d<D>(int, bool);
 FRA_HEAD_DIMS(FRA_EXTERN_BWD_D)

@@ -129,6 +129,62 @@ __device__ __forceinline__ void dma16(const void *src, uint32_t lds_addr) {
         : "memory");
 }
 
+// Up to five direct loads in one asm statement: load i moves, for the lanes
+// set in mask[i], the 16 bytes at base + off[i] (base uniform, off a 32-bit
+// lane offset: the SGPR-base form of the instruction) to LDS byte address
+// dst[i] + 16 * lane; a load with mask 0 moves nothing.  Lanes left out of a
+// load keep their LDS slot, so padding written once at set-up stays.  EXEC
+// and M0 (the destination, a register the compiler neither sees nor
+// preserves) are saved first and restored at the end; the s_nops are the
+// wait states after writing them.  The loads are the caller's to wait for
+// (s_waitcnt vmcnt and a barrier before the destination is read), and the
+// caller's control flow must be uniform (EXEC all ones or the same for the
+// whole statement).
+#define FRA_DMA_HEAD "s_mov_b64 %[se], exec\n\ts_mov_b32 %[sm], m0\n\t"
+#define FRA_DMA_ONE(i)                                                                                 \
+    "s_mov_b32 m0, %[d" #i "]\n\ts_mov_b64 exec, %[k" #i "]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[o" #i \
+    "], %[b]\n\t"
+#define FRA_DMA_TAIL "s_nop 0\n\ts_mov_b64 exec, %[se]\n\ts_mov_b32 m0, %[sm]"
+#define FRA_DMA_IN(i) [o##i] "v"(off[i]), [k##i] "s"(mask[i]), [d##i] "s"(dst[i])
+template <int N>
+__device__ __forceinline__ void dma_rows(const void *base, const uint32_t (&off)[N], const uint64_t (&mask)[N],
+                                         const uint32_t (&dst)[N]) {
+    static_assert(N >= 1 && N <= 5, "one to five loads");
+    uint64_t se;
+    uint32_t sm;
+    if constexpr (N == 1) {
+        asm volatile(FRA_DMA_HEAD FRA_DMA_ONE(0) FRA_DMA_TAIL
+                     : [se] "=&s"(se), [sm] "=&s"(sm)
+                     : [b] "s"(base), FRA_DMA_IN(0)
+                     : "memory");
+    } else if constexpr (N == 2) {
+        asm volatile(FRA_DMA_HEAD FRA_DMA_ONE(0) FRA_DMA_ONE(1) FRA_DMA_TAIL
+                     : [se] "=&s"(se), [sm] "=&s"(sm)
+                     : [b] "s"(base), FRA_DMA_IN(0), FRA_DMA_IN(1)
+                     : "memory");
+    } else if constexpr (N == 3) {
+        asm volatile(FRA_DMA_HEAD FRA_DMA_ONE(0) FRA_DMA_ONE(1) FRA_DMA_ONE(2) FRA_DMA_TAIL
+                     : [se] "=&s"(se), [sm] "=&s"(sm)
+                     : [b] "s"(base), FRA_DMA_IN(0), FRA_DMA_IN(1), FRA_DMA_IN(2)
+                     : "memory");
+    } else if constexpr (N == 4) {
+        asm volatile(FRA_DMA_HEAD FRA_DMA_ONE(0) FRA_DMA_ONE(1) FRA_DMA_ONE(2) FRA_DMA_ONE(3) FRA_DMA_TAIL
+                     : [se] "=&s"(se), [sm] "=&s"(sm)
+                     : [b] "s"(base), FRA_DMA_IN(0), FRA_DMA_IN(1), FRA_DMA_IN(2), FRA_DMA_IN(3)
+                     : "memory");
+    } else {
+        asm volatile(FRA_DMA_HEAD FRA_DMA_ONE(0) FRA_DMA_ONE(1) FRA_DMA_ONE(2) FRA_DMA_ONE(3) FRA_DMA_ONE(4)
+                         FRA_DMA_TAIL
+                     : [se] "=&s"(se), [sm] "=&s"(sm)
+                     : [b] "s"(base), FRA_DMA_IN(0), FRA_DMA_IN(1), FRA_DMA_IN(2), FRA_DMA_IN(3), FRA_DMA_IN(4)
+                     : "memory");
+    }
+}
+#undef FRA_DMA_HEAD
+#undef FRA_DMA_ONE
+#undef FRA_DMA_TAIL
+#undef FRA_DMA_IN
+
 // Compute units of the current device (host code; cached per device and
 // translation unit; 256 when no device can be queried, e.g. planning on a
 // host without a GPU).

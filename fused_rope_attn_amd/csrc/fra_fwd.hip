@@ -1,7 +1,7 @@
 // fra_fwd.hip -- forward dispatch and the C ABI of libfra.so (include/fra.h):
 // argument checks, kernel choice, workspace sizing and launches.  The
 // kernels themselves are in fra_fwd_kernels.h, compiled once per head_dim
-// by fra_inst.hip.
+// by fra_inst_fwd.hip.
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -240,7 +240,7 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true) {
             c.split_parts = sp.parts;
         }
         c.kernel = FRA_KERNEL_LONG;
-        c.block = kLongThreads;
+        c.block = kL4Threads;
         c.block_q = kLongBQ;
         c.block_kv = kLongBKV;
         snprintf(c.name, sizeof(c.name), "long_d%d_%s_rope%s", d, dtype_name(a->qkv_dtype),

@@ -1,12 +1,12 @@
 // fra_fwd_types.h -- forward types and constants shared by the dispatch
-// (fra_fwd.hip) and the per-head_dim kernel instances (fra_inst.hip).
+// (fra_fwd.hip) and the per-head_dim kernel instances (fra_inst_fwd.hip, fra_inst_bwd.hip).
 #pragma once
 
 #include <stdint.h>
 
 #include "fra.h"
 
-// Head dims with compiled kernels.  fra_inst.hip is compiled once per entry
+// Head dims with compiled kernels.  fra_inst_fwd.hip and fra_inst_bwd.hip are compiled once per entry
 // with -DFRA_HEAD_DIM=<D> (fused_rope_attn_amd/build.py reads this list);
 // each must be a multiple of 8 so that both halves of a row start on an
 // 8-byte boundary.  A build may pass its own list (-D'FRA_HEAD_DIMS(X)=...')
@@ -51,6 +51,8 @@ constexpr int kLongWaves = 8;
 constexpr int kLongBQ = 32 * kLongWaves;  // query rows per workgroup
 constexpr int kLongBKV = 64;              // key/value rows per stage
 constexpr int kLongThreads = 64 * kLongWaves;
+constexpr int kL4Waves = 4;                // the long kernel in use: four wavefronts of 64 query rows
+constexpr int kL4Threads = 64 * kL4Waves;
 
 // Split last round of the long kernel (see split_plan in fra_fwd.hip).
 // Workspace: per (split unit, part), kLongBQ rows of split_row_floats(D) floats:
@@ -82,7 +84,7 @@ struct Choice {
 };
 
 // Kernel instances of one head_dim (defined in fra_fwd_kernels.h,
-// instantiated by fra_inst.hip): fills c.fn (and the long kernel's merge,
+// instantiated by fra_inst_fwd.hip): fills c.fn (and the long kernel's merge,
 // PRE and krot instances) for a window (hw heads per workgroup) or long
 // layer; c.fn stays NULL when the combination has no kernel.
 template <int D> void pick_d(bool window, int hw, bool full, int qkv, int rd, Choice &c);

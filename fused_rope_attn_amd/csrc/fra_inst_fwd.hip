@@ -1,10 +1,11 @@
-// fra_inst.hip -- the forward and backward kernel instances of one head_dim.
+// fra_inst_fwd.hip -- the forward kernel instances of one head_dim.
 //
 // Compiled once per entry of FRA_HEAD_DIMS (fra_fwd_types.h) with
 // -DFRA_HEAD_DIM=<D>, so that the instances of different head dims build in
-// parallel; the dispatch units (fra_fwd.hip, fra_bwd.hip) reach them through
-// pick_d<D> and bwd_kernels_d<D>.
-#include "fra_bwd_kernels.h"
+// parallel; the dispatch unit (fra_fwd.hip) reaches them through pick_d<D>.
+// Built with MFMA results in VGPRs (-amdgpu-mfma-vgpr-form): the scores of
+// both kernels go straight to the vector unit's softmax, and the long
+// kernel's four wavefronts hold their O accumulators in AGPRs regardless.
 #include "fra_fwd_kernels.h"
 
 #ifndef FRA_HEAD_DIM
@@ -13,5 +14,4 @@
 
 namespace fra_internal {
 template void pick_d<FRA_HEAD_DIM>(bool, int, bool, int, int, Choice &);
-template BwdKernels bwd_kernels_d<FRA_HEAD_DIM>(int, bool);
 }  // namespace fra_internal
