@@ -44,6 +44,20 @@ struct BF16 {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
     }
+    // c += A B with c held in accumulation registers.  The compiler's hazard
+    // checks do not see an MFMA in inline asm, so the asm keeps its own: two
+    // wait states before it (its operands may come straight from the vector
+    // unit), and, with TAIL, 24 after it -- an 8-pass 32x32x16 result needs
+    // 10 before any other instruction reads or moves it.  Every access of c
+    // other than by mma_acc must follow a TAIL call.
+    template <bool TAIL = false>
+    static __device__ __forceinline__ void mma_acc(u32x4 a, u32x4 b, f32x16 &c) {
+        if constexpr (TAIL)
+            asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                         : "+a"(c) : "v"(a), "v"(b));
+        else
+            asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    }
 };
 
 struct F16 {
@@ -60,6 +74,14 @@ struct F16 {
     static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+    template <bool TAIL = false>
+    static __device__ __forceinline__ void mma_acc(u32x4 a, u32x4 b, f32x16 &c) {
+        if constexpr (TAIL)
+            asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                         : "+a"(c) : "v"(a), "v"(b));
+        else
+            asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
     }
 };
 

@@ -1910,7 +1910,13 @@ void long4_kernel(const KParams p) {
                 const int st = i / NDT, dt = i % NDT;
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    oacc[t][dt] = E::mma(vb[i % 3], pop[t][st], oacc[t][dt]);
+                    // (O in accumulation registers: the last MFMA of the
+                    // phase waits for its result, so that O may be read or
+                    // moved after it)
+                    if (i == NOP - 1 && t == 1)
+                        E::template mma_acc<true>(vb[i % 3], pop[t][st], oacc[t][dt]);
+                    else
+                        E::mma_acc(vb[i % 3], pop[t][st], oacc[t][dt]);
                     const int sl_ = 2 * i + t;
                     if (sl_ < NS3) {
 #pragma unroll
