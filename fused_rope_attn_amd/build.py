@@ -10,8 +10,7 @@ Translation units, compiled in parallel:
   the C ABI (no kernels);
 * ``fra_inst_fwd.hip`` and ``fra_inst_bwd.hip`` once per head_dim of
   ``FRA_HEAD_DIMS`` (``csrc/fra_fwd_types.h``), with ``-DFRA_HEAD_DIM=<D>``:
-  that head_dim's forward and backward kernels (the forward with MFMA results
-  in VGPRs, ``-mllvm -amdgpu-mfma-vgpr-form``, below head_dim 128).
+  that head_dim's forward and backward kernels.
 
 ``FRA_BUILD_DIMS=80,72`` (environment) builds only those head dims, for
 quicker iteration on a kernel; the library then reports every other head_dim
@@ -87,12 +86,8 @@ def units(tmpd: str) -> list:
         common = ["-DFRA_HEAD_DIMS(X)=" + " ".join(f"X({d})" for d in dims)]
     out = [(os.path.join(CSRC, s), os.path.join(tmpd, s + ".o"), common) for s in ("fra_fwd.hip", "fra_bwd.hip")]
     for d in dims:
-        # (head_dim 128 keeps the default MFMA form: with the VGPR form this
-        # ROCm 7.2 compiler crashes in its AGPR-copy rewrite pass on the long
-        # kernel without a workspace and full-width fp32 tables.)
-        vgpr_form = ["-mllvm", "-amdgpu-mfma-vgpr-form"] if d < 128 else []
         out.append((os.path.join(CSRC, "fra_inst_fwd.hip"), os.path.join(tmpd, f"fra_inst_fwd_d{d}.o"),
-                    common + [f"-DFRA_HEAD_DIM={d}"] + vgpr_form))
+                    common + [f"-DFRA_HEAD_DIM={d}"]))
         out.append((os.path.join(CSRC, "fra_inst_bwd.hip"), os.path.join(tmpd, f"fra_inst_bwd_d{d}.o"),
                     common + [f"-DFRA_HEAD_DIM={d}"]))
     return out

@@ -44,20 +44,6 @@ struct BF16 {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
     }
-    // c += A B with c held in accumulation registers.  The compiler's hazard
-    // checks do not see an MFMA in inline asm, so the asm keeps its own: two
-    // wait states before it (its operands may come straight from the vector
-    // unit), and, with TAIL, 24 after it -- an 8-pass 32x32x16 result needs
-    // 10 before any other instruction reads or moves it.  Every access of c
-    // other than by mma_acc must follow a TAIL call.
-    template <bool TAIL = false>
-    static __device__ __forceinline__ void mma_acc(u32x4 a, u32x4 b, f32x16 &c) {
-        if constexpr (TAIL)
-            asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
-                         : "+a"(c) : "v"(a), "v"(b));
-        else
-            asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
-    }
 };
 
 struct F16 {
@@ -74,14 +60,6 @@ struct F16 {
     static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-    }
-    template <bool TAIL = false>
-    static __device__ __forceinline__ void mma_acc(u32x4 a, u32x4 b, f32x16 &c) {
-        if constexpr (TAIL)
-            asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
-                         : "+a"(c) : "v"(a), "v"(b));
-        else
-            asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
     }
 };
 
@@ -150,62 +128,6 @@ __device__ __forceinline__ void dma16(const void *src, uint32_t lds_addr) {
         : "v"(src), "s"(m0v)
         : "memory");
 }
-
-// Up to five direct loads in one asm statement: load i moves, for the lanes
-// set in mask[i], the 16 bytes at base + off[i] (base uniform, off a 32-bit
-// lane offset: the SGPR-base form of the instruction) to LDS byte address
-// dst[i] + 16 * lane; a load with mask 0 moves nothing.  Lanes left out of a
-// load keep their LDS slot, so padding written once at set-up stays.  EXEC
-// and M0 (the destination, a register the compiler neither sees nor
-// preserves) are saved first and restored at the end; the s_nops are the
-// wait states after writing them.  The loads are the caller's to wait for
-// (s_waitcnt vmcnt and a barrier before the destination is read), and the
-// caller's control flow must be uniform (EXEC all ones or the same for the
-// whole statement).
-#define FRA_DMA_HEAD "s_mov_b64 %[se], exec\n\ts_mov_b32 %[sm], m0\n\t"
-#define FRA_DMA_ONE(i)                                                                                 \
-    "s_mov_b32 m0, %[d" #i "]\n\ts_mov_b64 exec, %[k" #i "]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[o" #i \
-    "], %[b]\n\t"
-#define FRA_DMA_TAIL "s_nop 0\n\ts_mov_b64 exec, %[se]\n\ts_mov_b32 m0, %[sm]"
-#define FRA_DMA_IN(i) [o##i] "v"(off[i]), [k##i] "s"(mask[i]), [d##i] "s"(dst[i])
-template <int N>
-__device__ __forceinline__ void dma_rows(const void *base, const uint32_t (&off)[N], const uint64_t (&mask)[N],
-                                         const uint32_t (&dst)[N]) {
-    static_assert(N >= 1 && N <= 5, "one to five loads");
-    uint64_t se;
-    uint32_t sm;
-    if constexpr (N == 1) {
-        asm volatile(FRA_DMA_HEAD FRA_DMA_ONE(0) FRA_DMA_TAIL
-                     : [se] "=&s"(se), [sm] "=&s"(sm)
-                     : [b] "s"(base), FRA_DMA_IN(0)
-                     : "memory");
-    } else if constexpr (N == 2) {
-        asm volatile(FRA_DMA_HEAD FRA_DMA_ONE(0) FRA_DMA_ONE(1) FRA_DMA_TAIL
-                     : [se] "=&s"(se), [sm] "=&s"(sm)
-                     : [b] "s"(base), FRA_DMA_IN(0), FRA_DMA_IN(1)
-                     : "memory");
-    } else if constexpr (N == 3) {
-        asm volatile(FRA_DMA_HEAD FRA_DMA_ONE(0) FRA_DMA_ONE(1) FRA_DMA_ONE(2) FRA_DMA_TAIL
-                     : [se] "=&s"(se), [sm] "=&s"(sm)
-                     : [b] "s"(base), FRA_DMA_IN(0), FRA_DMA_IN(1), FRA_DMA_IN(2)
-                     : "memory");
-    } else if constexpr (N == 4) {
-        asm volatile(FRA_DMA_HEAD FRA_DMA_ONE(0) FRA_DMA_ONE(1) FRA_DMA_ONE(2) FRA_DMA_ONE(3) FRA_DMA_TAIL
-                     : [se] "=&s"(se), [sm] "=&s"(sm)
-                     : [b] "s"(base), FRA_DMA_IN(0), FRA_DMA_IN(1), FRA_DMA_IN(2), FRA_DMA_IN(3)
-                     : "memory");
-    } else {
-        asm volatile(FRA_DMA_HEAD FRA_DMA_ONE(0) FRA_DMA_ONE(1) FRA_DMA_ONE(2) FRA_DMA_ONE(3) FRA_DMA_ONE(4)
-                         FRA_DMA_TAIL
-                     : [se] "=&s"(se), [sm] "=&s"(sm)
-                     : [b] "s"(base), FRA_DMA_IN(0), FRA_DMA_IN(1), FRA_DMA_IN(2), FRA_DMA_IN(3), FRA_DMA_IN(4)
-                     : "memory");
-    }
-}
-#undef FRA_DMA_HEAD
-#undef FRA_DMA_ONE
-#undef FRA_DMA_TAIL
-#undef FRA_DMA_IN
 
 // Compute units of the current device (host code; cached per device and
 // translation unit; 256 when no device can be queried, e.g. planning on a

@@ -240,7 +240,7 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true) {
             c.split_parts = sp.parts;
         }
         c.kernel = FRA_KERNEL_LONG;
-        c.block = kL4Threads;
+        c.block = kLongThreads;
         c.block_q = kLongBQ;
         c.block_kv = kLongBKV;
         snprintf(c.name, sizeof(c.name), "long_d%d_%s_rope%s", d, dtype_name(a->qkv_dtype),

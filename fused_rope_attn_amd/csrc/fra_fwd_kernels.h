@@ -1385,632 +1385,6 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
     }
 }
 
-// ---- long kernel ---------------------------------------------------------------
-//
-// Split-Q flash tiling for segments of any length.  A workgroup of four
-// wavefronts -- one per SIMD, so each has the whole 512-register budget --
-// owns 256 query rows of one (segment, head): wavefront w holds rows
-// 64w .. 64w + 63 as two 32-row tiles t, their rotated Q in registers as the
-// B operands of S^T = K_rot Q_rot^T.  The workgroup walks the segment's keys
-// in blocks of 64.  Each K_rot operand and each transposed V operand a
-// wavefront reads from LDS feeds one MFMA of each tile, so LDS bytes per
-// MFMA are half what 32-row wavefronts read.
-//
-// Iteration j (64-key block j), per wavefront:
-//   phase A  S(j+1) for both tiles on the matrix core (4 S MFMAs per 16-deep
-//            k-step), beside the exponentials of S(j) for its first three
-//            16-key steps on the vector unit;
-//   phase B  O^T += V(j)^T P(j)^T for both tiles, beside the last 16-key
-//            step's exponentials, the row maxima of S(j+1) and -- without a
-//            workspace -- the rotation of K(j+2) into LDS.
-// One barrier per iteration.  K_rot and V sit in LDS rings: with the
-// rotated-K workspace (PRE), direct loads (global_load_lds_dwordx4) fill a
-// 3-stage K_rot ring and a 3-stage V ring, each load two iterations ahead;
-// without it, each thread loads the raw K quads and cos/sin quads of block
-// j+3 into registers in iteration j, rotates them in iteration j+1 and
-// writes them to a 2-stage K_rot ring: K_rot never reaches HBM.
-//
-// Softmax: exp2 online softmax in the scale*log2(e) domain, the running max
-// moved (and O rescaled) only when a row max exceeds it by more than 2^8 (a
-// ballot over the wavefront; rare after the first block).  When head_dim
-// leaves padding columns in the last 32-column tile of V, column D holds
-// ones, so the PV MFMA also yields the row sum of the rounded P.
-
-static_assert(64 * kL4Waves == kLongBQ, "a unit is 256 query rows");
-
-template <int D, int RD, bool FULL, bool PRE> struct L4Lds {
-    static constexpr int RB = RD == FRA_DTYPE_F32 ? 4 : 2;
-    static constexpr int HALF = D / 2;
-    static constexpr int W = FULL ? D : D / 2;         // table width
-    static constexpr int DP = (D + 15) / 16 * 16;      // K_rot row padded to the MFMA k-step
-    static constexpr int S = DP / 16;                  // k-steps of S^T
-    static constexpr int KS = DP + 8;                  // K_rot row pitch, elements (2S+1 chunks: odd)
-    static constexpr int NDT = (D + 31) / 32;          // 32-row tiles of O^T
-    static constexpr int KCH = D / 8;                  // 16-byte chunks of a K or V row
-    static constexpr int KRC = KS / 8;                 // K_rot row pitch in 16-byte chunks
-    static constexpr int VPC = long_vpitch(4 * NDT);   // V row pitch in chunks (4 or 12 mod 16)
-    static constexpr bool kOnes = D % 32 != 0;         // V column D holds ones
-    static constexpr int kKrot = 64 * KS * 2;
-    static constexpr int kV = 64 * VPC * 16;
-    static constexpr int NK = PRE ? 3 : 2;             // K_rot stages
-    static constexpr int NV = NK * kKrot + 3 * kV <= kLdsLimit ? 3 : 2;  // V stages
-    static constexpr int kOffK = 0;
-    static constexpr int kOffV = NK * kKrot;
-    static constexpr int kBytes = kOffV + NV * kV;
-    static_assert(kBytes <= kLdsLimit, "long kernel LDS budget");
-    static constexpr int KI = KRC;                     // direct loads (64 slots each) of a K_rot block
-    static constexpr int VI = VPC;                     // ... of a V block
-    static constexpr int MK = (KI + kL4Waves - 1) / kL4Waves;  // K_rot loads per wavefront, at most
-    static constexpr int MV = (VI + kL4Waves - 1) / kL4Waves;
-    static constexpr int NQ = D / 8;                   // quads per half row
-    static constexpr int RQ = (64 * NQ + kL4Threads - 1) / kL4Threads;  // rotation quads per thread
-};
-
-template <int D, class E, int RD, bool FULL, bool PRE>
-__global__ __launch_bounds__(kL4Threads) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void long4_kernel(const KParams p) {
-    using LDS = L4Lds<D, RD, FULL, PRE>;
-    constexpr int HALF = LDS::HALF, S = LDS::S, KS = LDS::KS, NDT = LDS::NDT, RB = LDS::RB;
-    constexpr int KCH = LDS::KCH, KRC = LDS::KRC, VPC = LDS::VPC, NQ = LDS::NQ, RQ = LDS::RQ;
-    constexpr int NK = LDS::NK, NV = LDS::NV;
-    constexpr bool ONES = LDS::kOnes;
-    typedef short v4i16 __attribute__((ext_vector_type(4)));
-    typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-    typedef __attribute__((address_space(3))) void lds_void;
-    __shared__ __attribute__((aligned(16))) char lds[LDS::kBytes];
-    auto lds_addr = [&](uint32_t off) { return (uint32_t)(uintptr_t)(lds_void *)(lds + off); };
-
-    // Unit u = (segment, head, query block); workgroups past tail_first take
-    // part `part` of the key range of a unit of the split last round.
-    int u, part = 0, nparts = 1;
-    if ((int)blockIdx.x < p.tail_first) {
-        u = xcd_remap(blockIdx.x, p.tail_first);
-    } else {
-        const int t = xcd_remap(blockIdx.x - p.tail_first, gridDim.x - p.tail_first);
-        nparts = p.tail_split;
-        u = p.tail_first + t / nparts;
-        part = t - (t / nparts) * nparts;
-    }
-    const int sh = u / p.qblocks, qblk = u - sh * p.qblocks;
-    const int seg = sh / p.num_heads, head = sh - seg * p.num_heads;
-    int s0 = p.cu[seg], s1 = p.cu[seg + 1];
-    s0 = min(max(s0, 0), p.total);
-    s1 = min(max(s1, 0), p.total);
-    const int L = s1 - s0;
-    if (L <= 0 || qblk * kLongBQ >= L) return;  // uniform across the workgroup
-
-    const int tid = threadIdx.x;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int r = lane & 31, g = lane >> 5;
-    // Key blocks [b0, b1) of the segment are this workgroup's (all of them
-    // unless the unit is split); Lkv keys, possibly none.
-    const int nblk_all = (L + kLongBKV - 1) / kLongBKV;
-    const int b0 = part * nblk_all / nparts, b1 = (part + 1) * nblk_all / nparts;
-    const int Lkv = min(L, kLongBKV * b1) - kLongBKV * b0;
-    const int nblk = (Lkv + kLongBKV - 1) / kLongBKV;
-    const int nkv_last = Lkv - kLongBKV * (nblk - 1);  // keys of the last block (1..64)
-
-    const int64_t k0 = (int64_t)s0 + (int64_t)kLongBKV * b0;  // first key row
-    const float sl = p.scale_log2;
-    float m_i[2] = {kNegInf, kNegInf}, l_i[2] = {0.f, 0.f};  // per tile: running max (scale*log2e units), row sum
-    f32x16 oacc[2][NDT];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) oacc[t][dt] = f32x16{};
-
-    if (Lkv > 0) {  // uniform; a part of a split unit may have no keys
-
-    // ---- one-time LDS set-up: the padding columns of every stage, which no
-    // load or rotation writes: K_rot zero, V zero with column D ones.
-    for (int i = tid; i < NK * 64 * (KS - D); i += kL4Threads) {
-        const int st = i / (64 * (KS - D)), rem = i - st * 64 * (KS - D);
-        const int row = rem / (KS - D), col = D + rem % (KS - D);
-        *(u16 *)(lds + LDS::kOffK + st * LDS::kKrot + (row * KS + col) * 2) = 0;
-    }
-    if constexpr (VPC > KCH) {
-        constexpr int PADC = VPC - KCH;
-        const u32 one = E::pack(1.0f, 0.0f) & 0xffffu;
-        for (int i = tid; i < NV * 64 * PADC; i += kL4Threads) {
-            const int st = i / (64 * PADC), rem = i - st * 64 * PADC;
-            const int row = rem / PADC, pc = rem - row * PADC;
-            u32x4 val = {0u, 0u, 0u, 0u};
-            if (ONES && pc == 0) val[0] = one;
-            *(u32x4 *)(lds + LDS::kOffV + st * LDS::kV + row * (VPC * 16) + (KCH + pc) * 16) = val;
-        }
-    }
-
-    // ---- direct loads -----------------------------------------------------------
-    // A block of a region with row pitch PC chunks (of which DC hold data) is
-    // PC direct loads of 64 slots: slot s = 64 gi + lane is chunk s % PC of row
-    // s / PC.  Wavefront w issues loads gi = w, w + 4, ...  A lane's offset is
-    // the same in every block; rows past a partial last block repeat its last
-    // row (their keys are masked).
-    const char *vbase = p.v + (k0 * p.sv_s + (int64_t)head * p.sv_h) * 2;
-    const uint32_t vrs = (uint32_t)(p.sv_s * 2);
-    const char *kbase = PRE ? p.krot + (k0 * p.num_heads + head) * (int64_t)(D * 2)
-                            : p.k + (k0 * p.sk_s + (int64_t)head * p.sk_h) * 2;
-    const uint32_t krs = PRE ? (uint32_t)(p.num_heads * D * 2) : (uint32_t)(p.sk_s * 2);
-    // Job m of wavefront w is load gi = w + 4m of a block: each lane's offset
-    // from the block's base is the same in every block; padding slots, and
-    // loads past the region, are masked off (their LDS slots keep the
-    // padding written above).  A partial last block's rows past its end
-    // repeat its last row (their keys are masked).
-    auto job = [&](int gi, int ni, int pc, uint32_t rs, int rows_valid, uint32_t &off, uint64_t &mask) {
-        const int s = 64 * gi + lane, row = s / pc, c = s - row * pc;
-        off = (uint32_t)min(row, rows_valid - 1) * rs + (uint32_t)(16 * c);
-        mask = gi < ni ? __builtin_amdgcn_ballot_w64(c < KCH) : 0ull;
-    };
-    uint32_t voff[LDS::MV], koff[LDS::MK];
-    uint64_t vmask[LDS::MV], kmask[LDS::MK];
-#pragma unroll
-    for (int m = 0; m < LDS::MV; ++m) job(w + kL4Waves * m, LDS::VI, VPC, vrs, kLongBKV, voff[m], vmask[m]);
-    if constexpr (PRE) {
-#pragma unroll
-        for (int m = 0; m < LDS::MK; ++m) job(w + kL4Waves * m, LDS::KI, KRC, krs, kLongBKV, koff[m], kmask[m]);
-    }
-    // The loads of one region's block x into the stage at dst0 (one asm
-    // statement, no branch per load).
-    auto dma_block = [&](const char *base, uint32_t rs, int pc, const auto &off, const auto &mask, int ni,
-                         uint32_t dst0, int x) {
-        constexpr int NJ = sizeof(off) / sizeof(off[0]);
-        uint32_t dst[NJ];
-#pragma unroll
-        for (int m = 0; m < NJ; ++m) dst[m] = __builtin_amdgcn_readfirstlane(lds_addr(dst0 + 1024 * (w + kL4Waves * m)));
-        const char *src = base + (int64_t)x * kLongBKV * rs;
-        if (x == nblk - 1 && nkv_last < kLongBKV) {  // uniform, last block only
-            uint32_t o2[NJ];
-            uint64_t k2[NJ];
-#pragma unroll
-            for (int m = 0; m < NJ; ++m) job(w + kL4Waves * m, ni, pc, rs, nkv_last, o2[m], k2[m]);
-            dma_rows(src, o2, k2, dst);
-        } else {
-            dma_rows(src, off, mask, dst);
-        }
-    };
-    auto dma_v = [&](int x, int st) {
-        if (x < nblk) dma_block(vbase, vrs, VPC, voff, vmask, LDS::VI, LDS::kOffV + st * LDS::kV, x);
-    };
-    auto dma_k = [&](int x, int st) {
-        if constexpr (PRE)
-            if (x < nblk) dma_block(kbase, krs, KRC, koff, kmask, LDS::KI, LDS::kOffK + st * LDS::kKrot, x);
-    };
-
-    // ---- K rotation in registers (no workspace) --------------------------------
-    // Thread tid rotates quads qi = tid + 256 m of a block (row qi / NQ, quad
-    // qi % NQ): raw quads of both halves and their cos/sin quads are loaded
-    // into registers in iteration x - 3 and rotated into the K_rot ring in
-    // iteration x - 2.
-    u32x2 rk0[RQ], rk1[RQ];
-    f32x4 rc0[RQ], rs0[RQ], rc1[RQ], rs1[RQ];
-    const char *cbase = p.cos + k0 * p.sr_s * RB, *sbase = p.sin + k0 * p.sr_s * RB;
-    const uint32_t trs = (uint32_t)(p.sr_s * RB);
-    auto raw_load = [&](int x) {
-        if constexpr (!PRE) {
-            if (x >= nblk) return;
-            const bool partial = x == nblk - 1 && nkv_last < kLongBKV;
-            const char *kb = kbase + (int64_t)x * kLongBKV * krs;
-            const char *cb = cbase + (int64_t)x * kLongBKV * trs, *sb = sbase + (int64_t)x * kLongBKV * trs;
-#pragma unroll
-            for (int m = 0; m < RQ; ++m) {
-                const int qi = tid + kL4Threads * m;
-                if (64 * NQ % kL4Threads == 0 || qi < 64 * NQ) {
-                    int row = qi / NQ;
-                    const int i = qi - row * NQ;
-                    if (partial) row = min(row, nkv_last - 1);
-                    const char *kr = kb + (uint32_t)row * krs;
-                    rk0[m] = *(const u32x2 *)(kr + 8 * i);
-                    rk1[m] = *(const u32x2 *)(kr + 2 * HALF + 8 * i);
-                    const char *cr = cb + (uint32_t)row * trs, *sr = sb + (uint32_t)row * trs;
-                    rc0[m] = Rope<RD>::quad(cr + RB * 4 * i);
-                    rs0[m] = Rope<RD>::quad(sr + RB * 4 * i);
-                    if constexpr (FULL) {
-                        rc1[m] = Rope<RD>::quad(cr + RB * (HALF + 4 * i));
-                        rs1[m] = Rope<RD>::quad(sr + RB * (HALF + 4 * i));
-                    }
-                }
-            }
-        }
-    };
-    // Quad m of this thread's share of block x, rotated into K_rot stage st
-    // (x < nblk is checked by the caller's uniform branch where it matters:
-    // past the last block the registers hold stale finite values and the
-    // stage is never read).
-    auto raw_rotate_quad = [&](int x, int st, int m) {
-        if constexpr (!PRE) {
-            const int qi = tid + kL4Threads * m;
-            if (64 * NQ % kL4Threads == 0 || qi < 64 * NQ) {
-                const int row = qi / NQ, i = qi - row * NQ;
-                char *kr = lds + LDS::kOffK + st * LDS::kKrot;
-                u32x2 a0, a1;
-                rotate_quad<E>(rk0[m], rk1[m], rc0[m], rs0[m], FULL ? rc1[m] : rc0[m], FULL ? rs1[m] : rs0[m], a0, a1);
-                *(u32x2 *)(kr + (row * KS + 4 * i) * 2) = a0;
-                *(u32x2 *)(kr + (row * KS + HALF + 4 * i) * 2) = a1;
-            }
-            (void)x;
-        }
-    };
-    auto raw_rotate = [&](int x, int st) {
-        if constexpr (!PRE) {
-            if (x >= nblk) return;
-#pragma unroll
-            for (int m = 0; m < RQ; ++m) raw_rotate_quad(x, st, m);
-        }
-    };
-
-    // ---- prologue: blocks 0.. in flight, Q_rot in registers, S(0) ------------------
-    if constexpr (PRE) {
-#pragma unroll
-        for (int x = 0; x < NK; ++x) dma_k(x, x);
-    } else {
-        raw_load(0);
-    }
-#pragma unroll
-    for (int x = 0; x < NV - 1; ++x) dma_v(x, x);
-
-    // Q_rot of this lane's query rows (tile t: row 64w + 32t + r), natural
-    // order [x0r | x1r | 0], as the B operands of S^T: k-step s, group g takes
-    // elements 16s + 8g .. +7.
-    u32x4 qop[2][S];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int q = qblk * kLongBQ + 64 * w + 32 * t + r;
-        const bool valid = q < L;
-        const int64_t row = s0 + (valid ? q : 0);
-        const char *qrow = p.q + (row * p.sq_s + (int64_t)head * p.sq_h) * 2;
-        const char *crow = p.cos + row * p.sr_s * RB;
-        const char *srow = p.sin + row * p.sr_s * RB;
-        u32x2 nat[LDS::DP / 4];
-#pragma unroll
-        for (int i = 0; i < NQ; ++i)
-            load_rotate_quad<D, E, RD, FULL>(qrow, crow, srow, i, valid, nat[i], nat[NQ + i]);
-#pragma unroll
-        for (int i = 2 * NQ; i < LDS::DP / 4; ++i) nat[i] = u32x2{0u, 0u};
-        const u32 msk = 0u - (u32)g;  // bitwise select: an index by g would move nat to scratch
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const u32x2 a = (nat[4 * s] & ~msk) | (nat[4 * s + 2] & msk);
-            const u32x2 b = (nat[4 * s + 1] & ~msk) | (nat[4 * s + 3] & msk);
-            qop[t][s] = u32x4{a[0], a[1], b[0], b[1]};
-        }
-    }
-    if constexpr (!PRE) {
-        // K_rot(0) now, K(1) loaded and rotated next, K(2), K(3) in flight.
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        raw_rotate(0, 0);
-        raw_load(1);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        raw_rotate(1, 1);
-        raw_load(2);
-    }
-
-    // Per-lane LDS byte offsets.  K_rot A operand of S^T: row 32a + r,
-    // elements 16s + 8g.  V transposed reads: the 16-lane group G = lane >> 4
-    // covers keys 4g + e (e = (lane >> 2) & 3) and columns 16 (G & 1) +
-    // 4 (lane & 3) of each 32-column tile.
-    const uint32_t k_lane = (uint32_t)(LDS::kOffK + (r * KS + 8 * g) * 2);
-    const uint32_t v_lane = (uint32_t)(LDS::kOffV + (4 * g + ((lane >> 2) & 3)) * (VPC * 16) +
-                                       2 * (16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
-
-    // S^T of both tiles from K_rot stage kst: sacc[t][a] (a: keys 32a..).
-    auto qk_all = [&](int kst, f32x16 (&sacc)[2][2]) {
-        const char *kb = lds + k_lane + kst * LDS::kKrot;
-#pragma unroll
-        for (int a = 0; a < 2; ++a) {
-#pragma unroll
-            for (int s = 0; s < S; ++s) {
-                const u32x4 kr = *(const u32x4 *)(kb + a * (32 * KS * 2) + 32 * s);
-#pragma unroll
-                for (int t = 0; t < 2; ++t) sacc[t][a] = E::mma(kr, qop[t][s], s == 0 ? f32x16{} : sacc[t][a]);
-            }
-        }
-    };
-    // Keys past a partial block: -inf.  Element jj of sacc[t][a] is key
-    // 32a + 8(jj/4) + 4g + (jj%4).
-    // (The lane's key offset is made opaque here: otherwise the compiler
-    // hoists the 64 loop-invariant compares out of the loop as lane masks,
-    // which spill the scalar registers.)
-    auto mask = [&](f32x16 (&sacc)[2][2], int nkv) {
-        const int lim = fresh(nkv - 4 * g);
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int a = 0; a < 2; ++a)
-#pragma unroll
-                for (int jj = 0; jj < 16; ++jj)
-                    if (32 * a + 8 * (jj >> 2) + (jj & 3) >= lim) sacc[t][a][jj] = kNegInf;
-    };
-    float mx[2];  // row maxima of the block whose exponentials come next
-    // Row max of tile t of a block's S^T (both key tiles, both lane halves),
-    // in scale*log2e units, in 12 pieces that phase B spreads over its MFMA
-    // slots: pieces 0-9 are max3 of elements 3k .. 3k+2, piece 10 the last
-    // two, piece 11 the tree, the exchange with lane^32 and the scale.
-    float mpart[2][11];
-    auto max_piece = [&](const f32x16 (&st)[2], int t, int k) {
-        if (k < 10) {
-            const int e = 3 * k;
-            mpart[t][k] = max3f(st[e >> 4][e & 15], st[(e + 1) >> 4][(e + 1) & 15], st[(e + 2) >> 4][(e + 2) & 15]);
-        } else if (k == 10) {
-            mpart[t][10] = fmaxf(st[1][14], st[1][15]);
-        } else {
-            const float u0 = max3f(mpart[t][0], mpart[t][1], mpart[t][2]);
-            const float u1 = max3f(mpart[t][3], mpart[t][4], mpart[t][5]);
-            const float u2 = max3f(mpart[t][6], mpart[t][7], mpart[t][8]);
-            const float u3 = fmaxf(mpart[t][9], mpart[t][10]);
-            mx[t] = max_pair32(fmaxf(max3f(u0, u1, u2), u3)) * sl;
-        }
-    };
-    auto rowmax_all = [&](const f32x16 (&st)[2][2]) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int k = 0; k < 12; ++k) max_piece(st[t], t, k);
-    };
-    // Lazy rescale: moves the running max of a tile (and scales its O and
-    // row sum) only when a row max exceeds it by more than the threshold.
-    auto rescale = [&]() {
-        const bool need = mx[0] > m_i[0] + kRescaleThreshold || mx[1] > m_i[1] + kRescaleThreshold;
-        if (__builtin_amdgcn_ballot_w64(need) != 0) {
-            // (an asm statement cannot be speculated: it keeps this rare
-            // block a branch instead of an unconditional multiply by a
-            // selected factor of every accumulator in every iteration)
-            asm volatile("");
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const float m_new = fmaxf(m_i[t], mx[t]);
-                const float alpha = __builtin_amdgcn_exp2f(m_i[t] - m_new);
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) oacc[t][dt] *= alpha;
-                l_i[t] *= alpha;
-                m_i[t] = m_new;
-            }
-        }
-    };
-    // exp2 of the 8 elements of 16-key step st (a = st / 2, half h = st % 2)
-    // of tile t, packed as the B operand of that PV step.
-    float lsum[2];
-    auto expo = [&](f32x16 (&cur)[2][2], int t, int st, int e) {  // element e (0..7) of (t, st)
-        const int a = st >> 1, jj = 8 * (st & 1) + e;
-        const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(cur[t][a][jj], sl, -m_i[t]));
-        cur[t][a][jj] = x;
-        if constexpr (!ONES) lsum[t] += x;
-    };
-    auto pack = [&](const f32x16 (&cur)[2][2], int t, int st) {
-        const int a = st >> 1, b = 8 * (st & 1);
-        return u32x4{E::pack(cur[t][a][b + 0], cur[t][a][b + 1]), E::pack(cur[t][a][b + 2], cur[t][a][b + 3]),
-                     E::pack(cur[t][a][b + 4], cur[t][a][b + 5]), E::pack(cur[t][a][b + 6], cur[t][a][b + 7])};
-    };
-    // V^T operand of PV step st, O^T tile dt, from V stage vst.
-    auto vop = [&](int vst, int st, int dt) {
-        const char *cp = lds + v_lane + vst * LDS::kV + 16 * st * (VPC * 16) + 64 * dt;
-        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)cp);
-        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(cp + 8 * (VPC * 16)));
-        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-        return u32x4{l2[0], l2[1], h2[0], h2[1]};
-    };
-
-    f32x16 sA[2][2], sB[2][2];
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    qk_all(0, sA);
-    if (nblk == 1 && nkv_last < kLongBKV) mask(sA, nkv_last);
-    rowmax_all(sA);
-    rescale();
-
-    // Iteration j.  cur holds S(j) (row max known, m_i set); nxt receives
-    // S(j+1) when NEXT.  kst/vst: stages of K_rot(j+1) and V(j).
-    // Direct loads a wavefront issues in an iteration whose blocks all exist
-    // (the fewest of any wavefront: waiting for more outstanding loads than a
-    // wavefront issued only waits longer).
-    constexpr int kDmaPerIter = (PRE ? LDS::KI / kL4Waves : 0) + LDS::VI / kL4Waves;
-    bool prev_full = false;  // the previous iteration issued all its loads
-
-    // Iteration j.  cur holds S(j) (row max known, m_i set); nxt receives
-    // S(j+1) when NEXT.  kst/vst: stages of K_rot(j+1) and V(j).
-    auto iteration = [&](auto next_tag, int j, int kst, int vst, f32x16 (&cur)[2][2], f32x16 (&nxt)[2][2]) {
-        constexpr bool NEXT = decltype(next_tag)::value;
-        // Every wavefront has finished iteration j - 1 (whose buffers this
-        // iteration's loads reuse), and what this iteration reads has landed:
-        // the loads of iteration j - 2 (with the rotated-K workspace, those of
-        // iteration j - 1 are for blocks read in iteration j + 1 and may stay
-        // in flight; without it, a raw K block is loaded one iteration ahead).
-        if (PRE && NK >= 3 && NV >= 3 && prev_full) {
-            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kDmaPerIter) : "memory");
-        } else {
-            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        }
-        prev_full = j + NK < nblk && j + NV - 1 < nblk;
-        // Loads: K_rot(j + NK) into the stage K_rot(j) had, V(j + NV - 1) into
-        // V(j - 1)'s; issued after the first MFMAs of phase A, which they
-        // then overlap.
-        int ks2 = kst + NK - 1;  // stage of K_rot(j) = stage of K_rot(j+1) - 1
-        if (ks2 >= NK) ks2 -= NK;
-        int vs2 = vst + NV - 1;
-        if (vs2 >= NV) vs2 -= NV;
-        auto issue_loads = [&]() {
-            dma_k(j + NK, ks2);
-            dma_v(j + NV - 1, vs2);
-        };
-        u32x4 pop[2][4];
-        if constexpr (!ONES) lsum[0] = lsum[1] = 0.f;
-        // exp2 of element e (0..7) of 16-key step st of tile t, and the pack
-        // of a finished step (materialised where it is computed: left alone,
-        // the compiler sinks the exponentials to the PV MFMAs).
-        auto expo_item = [&](int t, int st, int e) {
-            expo(cur, t, st, e);
-            if (e == 7) {
-                pop[t][st] = pack(cur, t, st);
-                asm volatile("" : "+v"(pop[t][st]));
-            }
-        };
-        // Phase A: S(j+1) on the matrix core beside the exponentials of the
-        // first three 16-key steps of S(j).
-        if constexpr (NEXT) {
-            constexpr int NA = 2 * S;  // (a, s) pairs, operand read two ahead
-            const char *kb = lds + k_lane + kst * LDS::kKrot;
-            auto kaddr = [&](int i) { return kb + (i & 1) * (32 * KS * 2) + 32 * (i >> 1); };
-            u32x4 kr[3];
-            kr[0] = *(const u32x4 *)kaddr(0);
-            if (NA > 1) kr[1] = *(const u32x4 *)kaddr(1);
-            constexpr int NE = 2 * 3 * 8;  // exponentials in phase A
-#pragma unroll
-            for (int i = 0; i < NA; ++i) {
-                if (i + 2 < NA) kr[(i + 2) % 3] = *(const u32x4 *)kaddr(i + 2);
-                const int a = i & 1, s = i >> 1;
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    nxt[t][a] = E::mma(kr[i % 3], qop[t][s], s == 0 ? f32x16{} : nxt[t][a]);
-                    const int mi = 2 * i + t;  // MFMA index 0 .. 2NA-1
-#pragma unroll
-                    for (int e = NE * mi / (2 * NA); e < NE * (mi + 1) / (2 * NA); ++e)
-                        expo_item(e / 24, (e % 24) / 8, e % 8);
-                }
-                if (i == 0) issue_loads();
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        } else {
-            issue_loads();
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int st = 0; st < 3; ++st)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) expo_item(t, st, e);
-        }
-        if constexpr (NEXT) {
-            if (j + 1 == nblk - 1 && nkv_last < kLongBKV) {  // uniform, last block only
-                asm volatile("");  // a branch, not selects in every iteration
-                mask(nxt, nkv_last);
-            }
-        }
-        // Phase B: PV(j), V^T operands read two steps ahead, beside the last
-        // step's exponentials, the row max of S(j+1) in pieces and the
-        // rotation of K(j+2).  The 16 exponentials (and the two packs) are
-        // spread over the MFMA slots before step 3, whose B operands they
-        // make; the other work items over all slots.
-        {
-            constexpr int NOP = 4 * NDT;   // V^T operands: (step st, tile dt)
-            constexpr int NSLOT = 2 * NOP;  // PV MFMAs
-            constexpr int NS3 = 2 * 3 * NDT;  // slots before step 3
-            constexpr int NW_EXP = 16, NW_MAX = NEXT ? 24 : 0, NW_ROT = PRE ? 0 : RQ;
-            constexpr int NW = NW_MAX + NW_ROT;
-            auto work = [&](int k) {
-                if (k < NW_MAX) {
-                    if constexpr (NEXT) max_piece(nxt[k / 12], k / 12, k % 12);
-                } else {
-                    if constexpr (!PRE) raw_rotate_quad(j + 2, ks2, k - NW_MAX);
-                }
-            };
-            u32x4 vb[3];
-            vb[0] = vop(vst, 0, 0);
-            if (NOP > 1) vb[1] = vop(vst, 1 / NDT, 1 % NDT);
-#pragma unroll
-            for (int i = 0; i < NOP; ++i) {
-                if (i + 2 < NOP) vb[(i + 2) % 3] = vop(vst, (i + 2) / NDT, (i + 2) % NDT);
-                const int st = i / NDT, dt = i % NDT;
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    // (O in accumulation registers: the last MFMA of the
-                    // phase waits for its result, so that O may be read or
-                    // moved after it)
-                    if (i == NOP - 1 && t == 1)
-                        E::template mma_acc<true>(vb[i % 3], pop[t][st], oacc[t][dt]);
-                    else
-                        E::mma_acc(vb[i % 3], pop[t][st], oacc[t][dt]);
-                    const int sl_ = 2 * i + t;
-                    if (sl_ < NS3) {
-#pragma unroll
-                        for (int e = (NW_EXP * sl_ + NS3 - 1) / NS3; e < (NW_EXP * (sl_ + 1) + NS3 - 1) / NS3; ++e)
-                            expo_item(e / 8, 3, e % 8);
-                    }
-#pragma unroll
-                    for (int k = (NW * sl_ + NSLOT - 1) / NSLOT; k < (NW * (sl_ + 1) + NSLOT - 1) / NSLOT; ++k)
-                        work(k);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            if constexpr (!PRE) raw_load(j + 3);
-        }
-        if constexpr (!ONES) {
-            l_i[0] += sum_pair32(lsum[0]);
-            l_i[1] += sum_pair32(lsum[1]);
-        }
-        if constexpr (NEXT) rescale();
-    };
-    typedef BoolTag<true> Next;
-    typedef BoolTag<false> Last;
-
-    int j = 0, kst = 1 % NK, vst = 0;  // stages of K_rot(j+1) and V(j)
-    auto adv = [&]() {
-        kst = kst + 1 == NK ? 0 : kst + 1;
-        vst = vst + 1 == NV ? 0 : vst + 1;
-    };
-    for (; j + 2 < nblk; j += 2) {
-        iteration(Next{}, j, kst, vst, sA, sB);
-        adv();
-        iteration(Next{}, j + 1, kst, vst, sB, sA);
-        adv();
-    }
-    if (j + 1 < nblk) {
-        iteration(Next{}, j, kst, vst, sA, sB);
-        adv();
-        iteration(Last{}, j + 1, kst, vst, sB, sA);
-    } else {
-        iteration(Last{}, j, kst, vst, sA, sB);
-    }
-
-    }  // Lkv > 0
-
-    if constexpr (ONES) {
-        // O^T row D (the ones column of V) is element 4*((D % 32) / 8) of the
-        // last d tile, held by the g = 0 lanes.
-        constexpr int jl = 4 * ((D - 32 * (NDT - 1)) / 8);
-        l_i[0] = bcast_lo32(oacc[0][NDT - 1][jl]);
-        l_i[1] = bcast_lo32(oacc[1][NDT - 1][jl]);
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int row = 64 * w + 32 * t + r;  // row of the unit
-        const int q = qblk * kLongBQ + row;
-        if (nparts > 1) {
-            if (q < L) {
-                constexpr int RF = split_row_floats(D);
-                float *prow = (float *)p.ws + ((int64_t)((u - p.tail_first) * nparts + part) * kLongBQ + row) * RF;
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-                    for (int jq = 0; jq < 4; ++jq) {
-                        const int d0 = 32 * dt + 8 * jq + 4 * g;
-                        if (d0 < D)
-                            *(f32x4 *)(prow + d0) = f32x4{oacc[t][dt][4 * jq + 0], oacc[t][dt][4 * jq + 1],
-                                                          oacc[t][dt][4 * jq + 2], oacc[t][dt][4 * jq + 3]};
-                    }
-                if (g == 0) {
-                    typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
-                    *(f32x2 *)(prow + D) = f32x2{m_i[t], l_i[t]};
-                }
-            }
-            continue;
-        }
-        if (q < L) {
-            const float inv = 1.0f / l_i[t];
-            if (p.lse != nullptr && g == 0)
-                p.lse[(int64_t)head * p.total + s0 + q] = (m_i[t] + __builtin_amdgcn_logf(l_i[t])) * kLn2;
-            char *orow = p.out + ((int64_t)(s0 + q) * p.so_s + (int64_t)head * p.so_h) * 2;
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-                for (int jq = 0; jq < 4; ++jq) {
-                    const int d0 = 32 * dt + 8 * jq + 4 * g;
-                    if (d0 < D)
-                        *(u32x2 *)(orow + 2 * d0) =
-                            u32x2{E::pack(oacc[t][dt][4 * jq + 0] * inv, oacc[t][dt][4 * jq + 1] * inv),
-                                  E::pack(oacc[t][dt][4 * jq + 2] * inv, oacc[t][dt][4 * jq + 3] * inv)};
-                }
-        }
-    }
-}
-
 }  // namespace
 
 namespace fra_internal {
@@ -2039,12 +1413,12 @@ template <int D, class E, int RD, bool FULL> void pick_full(bool window, int hw,
         }
     }
     if constexpr (long_ok<D, RD, FULL>()) {
-        c.fn = (KernelFn)long4_kernel<D, E, RD, FULL, false>;
+        c.fn = (KernelFn)long_kernel<D, E, RD, FULL, false>;
         c.merge = (KernelFn)split_merge_kernel<D, E>;
-        c.lds = L4Lds<D, RD, FULL, false>::kBytes;
-        c.fn_pre = (KernelFn)long4_kernel<D, E, RD, FULL, true>;
+        c.lds = LongLds<D, RD, FULL>::kBytes;
+        c.fn_pre = (KernelFn)long_kernel<D, E, RD, FULL, true>;
         c.krot = (KernelFn)krot_kernel<D, E, RD, FULL>;
-        c.lds_pre = L4Lds<D, RD, FULL, true>::kBytes;
+        c.lds_pre = LongLds<D, RD, FULL, true>::kBytes;
     }
 }
 

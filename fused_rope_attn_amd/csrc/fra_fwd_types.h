@@ -51,8 +51,6 @@ constexpr int kLongWaves = 8;
 constexpr int kLongBQ = 32 * kLongWaves;  // query rows per workgroup
 constexpr int kLongBKV = 64;              // key/value rows per stage
 constexpr int kLongThreads = 64 * kLongWaves;
-constexpr int kL4Waves = 4;                // the long kernel in use: four wavefronts of 64 query rows
-constexpr int kL4Threads = 64 * kL4Waves;
 
 // Split last round of the long kernel (see split_plan in fra_fwd.hip).
 // Workspace: per (split unit, part), kLongBQ rows of split_row_floats(D) floats:

@@ -3,9 +3,6 @@
 // Compiled once per entry of FRA_HEAD_DIMS (fra_fwd_types.h) with
 // -DFRA_HEAD_DIM=<D>, so that the instances of different head dims build in
 // parallel; the dispatch unit (fra_fwd.hip) reaches them through pick_d<D>.
-// Built with MFMA results in VGPRs (-amdgpu-mfma-vgpr-form): the scores of
-// both kernels go straight to the vector unit's softmax, and the long
-// kernel's four wavefronts hold their O accumulators in AGPRs regardless.
 #include "fra_fwd_kernels.h"
 
 #ifndef FRA_HEAD_DIM
