@@ -37,9 +37,9 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 from fused_rope_attn_amd import (fused_rope_attention, fused_rope_attention_bwd,  # noqa: E402
-                                 fused_rope_attention_fwd, plan)
+                                 fused_rope_attention_fwd, fused_rope_attention_pos, plan, plan_pos)
 from fused_rope_attn_amd.configs import (WORKLOADS, algorithmic_bytes, algorithmic_bytes_bwd,  # noqa: E402
-                                         algorithmic_flops, algorithmic_flops_bwd, make_inputs)
+                                         algorithmic_flops, algorithmic_flops_bwd, make_inputs, positions)
 
 METRIC = "µs/call fused RoPE+varlen attn (1344² window layer); % HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
@@ -300,6 +300,50 @@ def run_comparator(name: str, steps: int, warmup: int, flush: torch.Tensor, dev)
     return row
 
 
+def positions_call(w, inp, dev):
+    """A closure running ``fused_rope_attention_pos`` on the workload: the
+    same q, k, v and cu_seqlens, the rotation angles computed in the kernels
+    from the tokens' (h, w) positions instead of read from cos/sin."""
+    pos, inv = positions(w, dev)
+    q, k, v, cu = (inp[x] for x in ("q", "k", "v", "cu_seqlens"))
+    ms = inp["max_seqlen"]
+    out = torch.empty_like(q)
+
+    def call():
+        fused_rope_attention_pos(q, k, v, pos, inv, cu, ms, out=out)
+
+    return call, pos, inv
+
+
+def run_positions(name: str, steps: int, warmup: int, flush: torch.Tensor, dev) -> dict:
+    """The table op and the position variant on the same inputs, timed
+    alternately (table, positions, table, positions): cold medians."""
+    w = WORKLOADS[name]
+    inp = make_inputs(w, seed=1234 + list(WORKLOADS).index(name), device=dev)
+    q, k, v, cos, sin, cu = (inp[x] for x in ("q", "k", "v", "cos", "sin", "cu_seqlens"))
+    ms = inp["max_seqlen"]
+    out = torch.empty_like(q)
+
+    def tab():
+        fused_rope_attention(q, k, v, cos, sin, cu, ms, out=out)
+
+    posc, pos, inv = positions_call(w, inp, dev)
+    t1 = time_calls(tab, steps, warmup, flush)
+    p1 = time_calls(posc, steps, warmup, flush)
+    t2 = time_calls(tab, steps, warmup, flush)
+    p2 = time_calls(posc, steps, warmup, flush)
+    ref = fused_rope_attention(q, k, v, cos, sin, cu, ms)
+    got = fused_rope_attention_pos(q, k, v, pos, inv, cu, ms)
+    torch.cuda.synchronize()
+    tab_us = (t1["cold_median_us"] + t2["cold_median_us"]) / 2
+    pos_us = (p1["cold_median_us"] + p2["cold_median_us"]) / 2
+    return {"workload": name, "note": w.note, "kernel": plan_pos(q, k, v, pos, inv, cu, ms)["name"],
+            "tables_cold_us": tab_us, "positions_cold_us": pos_us, "positions_over_tables": pos_us / tab_us,
+            "tables_warm_us": (t1["warm_us"] + t2["warm_us"]) / 2,
+            "positions_warm_us": (p1["warm_us"] + p2["warm_us"]) / 2,
+            "max_abs_diff": float((ref.float() - got.float()).abs().max())}
+
+
 def run_backward(name: str, steps: int, warmup: int, flush: torch.Tensor, dev) -> dict:
     w = WORKLOADS[name]
     inp = make_inputs(w, seed=1234 + list(WORKLOADS).index(name), device=dev)
@@ -332,6 +376,8 @@ def profile_driver(args, flush, dev) -> int:
     out = torch.empty_like(q)
     if args.bwd:
         call = backward_call(inp)
+    elif args.pos:
+        call, _, _ = positions_call(w, inp, dev)
     elif args.floor:
         call = floor_call(inp)
     else:
@@ -357,6 +403,11 @@ def profile_driver(args, flush, dev) -> int:
         flops = algorithmic_flops_bwd(w.heads, w.head_dim, lens)
     if args.floor:
         nbytes = 4 * q.numel() * q.element_size()
+    if args.pos:
+        pos, inv = positions(w, dev)
+        pl = plan_pos(q, k, v, pos, inv, cu, inp["max_seqlen"])
+        # no tables read; the (h, w) positions and inv_freq instead
+        nbytes += n_tok * 8 + (w.head_dim // 4) * 4 - 2 * n_tok * cos.shape[1] * cos.element_size()
     print(json.dumps({"profile_driver": args.workload, "direction": "backward" if args.bwd else "forward",
                       "kernel": "floor: torch.addcmul(q, k, v)" if args.floor else pl["name"], "warmup_calls": 3,
                       "calls": args.profile_calls, "bytes": nbytes, "flops": flops,
@@ -543,6 +594,10 @@ def main() -> int:
     ap.add_argument("--floor", action="store_true",
                     help="time the floor probe (one elementwise kernel reading q, k, v and writing an output) on "
                          "--workload's tensors instead of the op (also a --profile-calls driver option)")
+    ap.add_argument("--positions", default=None, metavar="FILE",
+                    help="time the position variant (fused_rope_attention_pos) beside the table op for every "
+                         "workload and write them to FILE")
+    ap.add_argument("--pos", action="store_true", help="profiling driver: run the position variant instead")
     ap.add_argument("--drift", default=None, metavar="FILE",
                     help="run the 32-layer drift stack on --workload's grid and write the report to FILE")
     args = ap.parse_args()
@@ -567,6 +622,17 @@ def main() -> int:
                                                           for k, v in r.items() if k not in ("workload", "note")),
                   file=sys.stderr, flush=True)
         with open(args.comparator, "w") as f:
+            json.dump(rows, f, indent=1)
+        return 0
+    if args.positions:
+        rows = []
+        for name in WORKLOADS:
+            r = run_positions(name, max(10, args.steps // 2), max(3, args.warmup // 2), flush, dev)
+            rows.append(r)
+            print(f"[bench] positions {name}: tables {r['tables_cold_us']:.1f} us, positions "
+                  f"{r['positions_cold_us']:.1f} us ({r['positions_over_tables']:.3f}x), max-abs diff "
+                  f"{r['max_abs_diff']:.2e}", file=sys.stderr, flush=True)
+        with open(args.positions, "w") as f:
             json.dump(rows, f, indent=1)
         return 0
     if args.backward:

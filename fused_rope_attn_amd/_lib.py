@@ -93,11 +93,25 @@ class Plan(ctypes.Structure):
     ]
 
 
+class RopePositions(ctypes.Structure):
+    """Mirror of ``struct fra_rope_positions``."""
+
+    _fields_ = [
+        ("pos", ctypes.c_void_p),
+        ("inv_freq", ctypes.c_void_p),
+    ]
+
+
 # Every symbol include/fra.h declares, with its ctypes signature.
 SIGNATURES = {
     "fra_fwd_varlen": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.c_void_p]),
     "fra_fwd_varlen_static": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.c_void_p]),
     "fra_query_plan": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(Plan)]),
+    "fra_fwd_varlen_pos": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(RopePositions), ctypes.c_void_p]),
+    "fra_workspace_bytes_pos": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(RopePositions),
+                                               ctypes.POINTER(ctypes.c_int64)]),
+    "fra_query_plan_pos": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(RopePositions),
+                                          ctypes.POINTER(Plan)]),
     "fra_workspace_bytes": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(ctypes.c_int64)]),
     "fra_supports_head_dim": (ctypes.c_int, [ctypes.c_int32]),
     "fra_last_error": (ctypes.c_char_p, []),

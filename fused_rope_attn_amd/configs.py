@@ -27,7 +27,7 @@ from .fused_attn import compute_rope_2d
 from .utils import get_window_index
 
 __all__ = ["Workload", "WORKLOADS", "make_inputs", "algorithmic_bytes", "algorithmic_flops",
-           "algorithmic_bytes_bwd", "algorithmic_flops_bwd"]
+           "algorithmic_bytes_bwd", "algorithmic_flops_bwd", "positions"]
 
 
 @dataclass(frozen=True)
@@ -80,6 +80,23 @@ def layout(w: Workload, device="cpu", rope_dtype=torch.float32):
         sins.append(sin)
     cu = torch.cat(cus).to(torch.int32)
     return cu.to(device), torch.cat(coss).to(device), torch.cat(sins).to(device)
+
+
+def positions(w: Workload, device="cpu"):
+    """``(pos int32 [N, 2], inv_freq fp32 [head_dim // 4])`` of a workload
+    for ``fused_rope_attention_pos``: the (h, w) position of every row of
+    ``layout``'s tables, in the same order."""
+    from .fused_attn import rope_positions_2d
+    poss, inv = [], None
+    for grids, merge in w.groups:
+        grids = [tuple(g) for g in grids]
+        widx = None
+        if w.kind == "window":
+            widx, _ = get_window_index(grids, window_size=w.window_size, spatial_merge_size=merge,
+                                       patch_size=w.patch_size, device="cpu")
+        pos, inv = rope_positions_2d(grids, w.head_dim, merge, w.theta, "cpu", window_idx=widx)
+        poss.append(pos)
+    return torch.cat(poss).to(device), inv.to(device)
 
 
 def make_inputs(w: Workload, seed: int = 0, device="cpu", dtype=torch.bfloat16, rope_dtype=torch.float32,

@@ -85,13 +85,17 @@ const char *dtype_name(int dt) {
         case FRA_DTYPE_BF16: return "bf16";
         case FRA_DTYPE_F16: return "f16";
         case FRA_DTYPE_F32: return "f32";
+        case kRopePos: return "pos";
         default: return "?";
     }
 }
 
 // allow_pre false: the rotated-K part of a workspace is not used (K is
 // rotated in the long kernel); all of the workspace may hold split scratch.
-int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true) {
+// rope non-NULL: the position variant (fra_fwd_varlen_pos); the cos/sin
+// fields of args are then ignored.
+int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true,
+         const fra_rope_positions *rope = nullptr) {
     if (!a) return fail(FRA_EINVAL, "args is NULL");
     if (a->flags != 0) return fail(FRA_EINVAL, "flags must be 0, got %d", a->flags);
     if (a->num_heads <= 0) return fail(FRA_EINVAL, "num_heads must be positive, got %d", a->num_heads);
@@ -102,30 +106,43 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true) {
     if (a->max_seqlen < 1) return fail(FRA_EINVAL, "max_seqlen must be >= 1, got %d", a->max_seqlen);
     if (a->qkv_dtype != FRA_DTYPE_BF16 && a->qkv_dtype != FRA_DTYPE_F16)
         return fail(FRA_EINVAL, "qkv_dtype must be bf16 or f16, got %d", a->qkv_dtype);
-    if (a->rope_dtype != FRA_DTYPE_F32 && a->rope_dtype != FRA_DTYPE_BF16 && a->rope_dtype != FRA_DTYPE_F16)
-        return fail(FRA_EINVAL, "rope_dtype must be f32, bf16 or f16, got %d", a->rope_dtype);
+    const bool pos = rope != nullptr;
     const int d = a->head_dim;
-    if (a->rope_width != d / 2 && a->rope_width != d)
-        return fail(FRA_EINVAL, "rope_width must be head_dim/2=%d or head_dim=%d, got %d", d / 2, d, a->rope_width);
+    if (pos) {
+        if (!rope->pos || !rope->inv_freq) return fail(FRA_EINVAL, "rope positions or inv_freq is NULL");
+        if (d % 4) return fail(FRA_EINVAL, "head_dim must be a multiple of 4 for rope positions, got %d", d);
+        if (!aligned(rope->pos, 8) || !aligned(rope->inv_freq, 4))
+            return fail(FRA_EUNSUPPORTED, "rope positions must be 8-byte aligned and inv_freq 4-byte aligned");
+    } else {
+        if (a->rope_dtype != FRA_DTYPE_F32 && a->rope_dtype != FRA_DTYPE_BF16 && a->rope_dtype != FRA_DTYPE_F16)
+            return fail(FRA_EINVAL, "rope_dtype must be f32, bf16 or f16, got %d", a->rope_dtype);
+        if (a->rope_width != d / 2 && a->rope_width != d)
+            return fail(FRA_EINVAL, "rope_width must be head_dim/2=%d or head_dim=%d, got %d", d / 2, d, a->rope_width);
+    }
+    const int rd = pos ? kRopePos : a->rope_dtype;
+    const bool full = !pos && a->rope_width == d;
+    const int64_t rope_stride = pos ? 0 : a->rope_stride_seq;
     if (!(a->softmax_scale > 0.f) || a->softmax_scale == __builtin_inff())
         return fail(FRA_EINVAL, "softmax_scale must be finite and > 0, got %g", (double)a->softmax_scale);
-    if (!a->q || !a->k || !a->v || !a->cos || !a->sin || !a->out || !a->cu_seqlens)
+    if (!a->q || !a->k || !a->v || (!pos && (!a->cos || !a->sin)) || !a->out || !a->cu_seqlens)
         return fail(FRA_EINVAL, "a tensor pointer is NULL");
     const int64_t strides[9] = {a->q_stride_seq, a->q_stride_head, a->k_stride_seq, a->k_stride_head,
                                 a->v_stride_seq, a->v_stride_head, a->out_stride_seq, a->out_stride_head,
-                                a->rope_stride_seq};
+                                rope_stride};
     for (int i = 0; i < 9; ++i)
         if (strides[i] < 0) return fail(FRA_EINVAL, "strides must be >= 0");
 
     // The window kernel addresses 64 rows of a tensor with 32-bit offsets.
     const int64_t max_row_bytes = 2 * std::max(std::max(a->q_stride_seq, a->k_stride_seq),
                                                std::max(a->v_stride_seq, a->out_stride_seq));
-    const bool small_rows = 64 * max_row_bytes < ((int64_t)1 << 31) && 64 * 4 * a->rope_stride_seq < ((int64_t)1 << 31);
+    const bool small_rows = 64 * max_row_bytes < ((int64_t)1 << 31) && 64 * 4 * rope_stride < ((int64_t)1 << 31);
     const bool window = a->max_seqlen <= 64 && d <= kWindowMaxD && small_rows;
     memset(&c, 0, sizeof(c));
-    if (!pick_kernel(d, window, kWinHeadsMax, a->rope_width == d, a->qkv_dtype, a->rope_dtype, c))
+    if (!pick_kernel(d, window, kWinHeadsMax, full, a->qkv_dtype, rd, c))
         return fail(FRA_EUNSUPPORTED, "head_dim=%d has no compiled kernel (built:" FRA_HEAD_DIMS_STRING ")", d);
-    if (!c.fn)
+    if (pos && !window && !c.fn_pre)
+        return fail(FRA_EUNSUPPORTED, "head_dim=%d has no long kernel for rope positions", d);
+    if (!c.fn && !(pos && !window))
         return fail(FRA_EUNSUPPORTED,
                     "%s cos/sin of width %d (rows of %d bytes) cannot be staged by the long kernel, which "
                     "moves table rows in 16-byte chunks; pass float32 tables",
@@ -140,7 +157,7 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true) {
             return fail(FRA_EUNSUPPORTED,
                         "k must be 16-byte aligned with strides that are multiples of 8 elements "
                         "(segments longer than 64 tokens)");
-        if (!aligned(a->cos, 16) || !aligned(a->sin, 16) || (a->rope_stride_seq * re) % 16)
+        if (!pos && (!aligned(a->cos, 16) || !aligned(a->sin, 16) || (a->rope_stride_seq * re) % 16))
             return fail(FRA_EUNSUPPORTED,
                         "cos/sin must be 16-byte aligned with a row stride that is a multiple of 16 bytes "
                         "(segments longer than 64 tokens)");
@@ -150,11 +167,11 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true) {
     // chunks, fp32 tables in 16-byte quads and 16-bit tables in 8-byte quads.
     const int re = a->rope_dtype == FRA_DTYPE_F32 ? 4 : 2;
     if (!aligned(a->q, 8) || !aligned(a->k, 8) || !aligned(a->out, 8) || !aligned(a->v, 16) ||
-        !aligned(a->cos, 4 * re) || !aligned(a->sin, 4 * re))
+        (!pos && (!aligned(a->cos, 4 * re) || !aligned(a->sin, 4 * re))))
         return fail(FRA_EUNSUPPORTED, "tensor base pointers are not aligned (q/k/out 8 B, v 16 B, cos/sin %d B)", 4 * re);
     if (a->q_stride_seq % 4 || a->q_stride_head % 4 || a->k_stride_seq % 4 || a->k_stride_head % 4 ||
         a->out_stride_seq % 4 || a->out_stride_head % 4 || a->v_stride_seq % 8 || a->v_stride_head % 8 ||
-        a->rope_stride_seq % 4)
+        rope_stride % 4)
         return fail(FRA_EUNSUPPORTED,
                     "strides must be multiples of 4 elements (q/k/out/cos/sin) and 8 elements (v)");
 
@@ -173,7 +190,9 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true) {
     kp.sv_h = a->v_stride_head;
     kp.so_s = a->out_stride_seq;
     kp.so_h = a->out_stride_head;
-    kp.sr_s = a->rope_stride_seq;
+    kp.sr_s = rope_stride;
+    kp.pos = pos ? rope->pos : nullptr;
+    kp.inv_freq = pos ? rope->inv_freq : nullptr;
     kp.total = a->total_seq;
     kp.num_heads = a->num_heads;
     kp.num_seqs = a->num_seqs;
@@ -198,7 +217,7 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true) {
             const int64_t g2 = (int64_t)a->num_seqs * ((a->num_heads + 1) / 2);
             Choice c2;
             memset(&c2, 0, sizeof(c2));
-            pick_kernel(d, true, 2, a->rope_width == d, a->qkv_dtype, a->rope_dtype, c2);
+            pick_kernel(d, true, 2, full, a->qkv_dtype, rd, c2);
             if (g2 <= (int64_t)device_cus() * c2.per_cu) c = c2;
         }
         kp.qblocks = 1;
@@ -207,8 +226,7 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true) {
         c.block = 64 * c.heads;
         c.block_q = 64;
         c.block_kv = 64;
-        snprintf(c.name, sizeof(c.name), "window_d%d_%s_rope%s", d, dtype_name(a->qkv_dtype),
-                 dtype_name(a->rope_dtype));
+        snprintf(c.name, sizeof(c.name), "window_d%d_%s_rope%s", d, dtype_name(a->qkv_dtype), dtype_name(rd));
     } else {
         kp.qblocks = (a->max_seqlen + kLongBQ - 1) / kLongBQ;
         const int64_t units = sh * kp.qblocks;
@@ -231,6 +249,7 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true) {
             kp.ws = (char *)a->workspace + kr_bytes;
             ws_left -= kr_bytes;
         }
+
         grid = units;
         if (sp.parts > 1 && ws_left >= sp.bytes) {
             kp.tail_first = (int32_t)(units - sp.units);
@@ -243,8 +262,7 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true) {
         c.block = kLongThreads;
         c.block_q = kLongBQ;
         c.block_kv = kLongBKV;
-        snprintf(c.name, sizeof(c.name), "long_d%d_%s_rope%s", d, dtype_name(a->qkv_dtype),
-                 dtype_name(a->rope_dtype));
+        snprintf(c.name, sizeof(c.name), "long_d%d_%s_rope%s", d, dtype_name(a->qkv_dtype), dtype_name(rd));
     }
     if (grid > 0x7fffffff) return fail(FRA_EUNSUPPORTED, "grid of %lld workgroups is too large", (long long)grid);
     c.grid = (int)grid;
@@ -363,7 +381,24 @@ int fra_fwd_varlen_static(const fra_fwd_args *args, void *stream) {
     return launch(&a, c, kp, stream);
 }
 
-int fra_workspace_bytes(const fra_fwd_args *args, int64_t *bytes) {
+int fra_fwd_varlen_pos(const fra_fwd_args *args, const fra_rope_positions *rope, void *stream) {
+    if (!rope) return fail(FRA_EINVAL, "rope is NULL");
+    Choice c;
+    KParams kp;
+    const int rc = plan(args, c, kp, true, rope);
+    if (rc != FRA_OK) return rc;
+    if (c.kernel == FRA_KERNEL_LONG && !c.pre)
+        return fail(FRA_EUNSUPPORTED,
+                    "rope positions on segments longer than 64 tokens need the rotated-K part of a workspace "
+                    "(%lld bytes; fra_workspace_bytes_pos)", (long long)krot_workspace_bytes(args));
+    return launch(args, c, kp, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int workspace_bytes(const fra_fwd_args *args, const fra_rope_positions *rope, int64_t *bytes) {
     if (!bytes) return fail(FRA_EINVAL, "bytes is NULL");
     *bytes = 0;
     if (!args) return fail(FRA_EINVAL, "args is NULL");
@@ -372,7 +407,7 @@ int fra_workspace_bytes(const fra_fwd_args *args, int64_t *bytes) {
     a.workspace_bytes = 0;
     Choice c;
     KParams kp;
-    const int rc = plan(&a, c, kp);
+    const int rc = plan(&a, c, kp, true, rope);
     if (rc != FRA_OK) return rc;
     if (c.kernel == FRA_KERNEL_LONG) {
         const SplitPlan sp = split_plan((int64_t)a.num_seqs * a.num_heads * kp.qblocks, a.max_seqlen, a.head_dim);
@@ -382,11 +417,11 @@ int fra_workspace_bytes(const fra_fwd_args *args, int64_t *bytes) {
     return FRA_OK;
 }
 
-int fra_query_plan(const fra_fwd_args *args, fra_plan *out) {
+int query_plan(const fra_fwd_args *args, const fra_rope_positions *rope, fra_plan *out) {
     if (!out) return fail(FRA_EINVAL, "plan is NULL");
     Choice c;
     KParams kp;
-    const int rc = plan(args, c, kp);
+    const int rc = plan(args, c, kp, true, rope);
     if (rc != FRA_OK) return rc;
     out->kernel = c.kernel;
     out->grid = c.grid;
@@ -400,6 +435,24 @@ int fra_query_plan(const fra_fwd_args *args, fra_plan *out) {
     g_err[0] = 0;
     return FRA_OK;
 }
+
+}  // namespace
+
+extern "C" {
+
+int fra_workspace_bytes(const fra_fwd_args *args, int64_t *bytes) { return workspace_bytes(args, nullptr, bytes); }
+
+int fra_workspace_bytes_pos(const fra_fwd_args *args, const fra_rope_positions *rope, int64_t *bytes) {
+    if (!rope) return fail(FRA_EINVAL, "rope is NULL");
+    return workspace_bytes(args, rope, bytes);
+}
+
+int fra_query_plan_pos(const fra_fwd_args *args, const fra_rope_positions *rope, fra_plan *plan) {
+    if (!rope) return fail(FRA_EINVAL, "rope is NULL");
+    return query_plan(args, rope, plan);
+}
+
+int fra_query_plan(const fra_fwd_args *args, fra_plan *out) { return query_plan(args, nullptr, out); }
 
 int fra_supports_head_dim(int32_t head_dim) {
     Choice c;

@@ -51,6 +51,63 @@ namespace {
 
 using namespace fra_internal;
 
+// ---- rope from positions (fra_fwd_varlen_pos) ----------------------------------------
+//
+// The table of the position variant is never read: Rope<kRopePos> only
+// supplies the element size its (unused) addressing assumes.
+template <> struct Rope<kRopePos> {
+    static constexpr int kBytes = 4;
+    static __device__ __forceinline__ f32x4 quad(const char *) { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+};
+
+// cos and sin of quad i (columns 4i .. 4i + 3) of the table row of a token at
+// patch position (ph, pw), width D/2: column j < D/4 has the angle
+// ph * inv_freq[j], column D/4 + j the angle pw * inv_freq[j] -- one fp32
+// product each, the reference's outer product (compute_rope_2d,
+// fused_attn.py:109-116, then .cos() / .sin()).
+//
+// The cosine and sine come from the hardware's v_cos_f32 / v_sin_f32, which
+// take revolutions.  The angle's revolutions ang / (2 pi) are formed as an
+// unevaluated sum hi + lo (Cody and Waite's split of the constant: hi =
+// ang * c_hi rounded, lo = its rounding error, exact by FMA, plus
+// ang * c_lo), and only the fraction of hi (exact for |hi| < 2^23) plus lo
+// reaches the instruction, so no rounding of the reduction is ever larger
+// than one ulp of the fraction.
+constexpr float kInv2PiHi = 0.15915494f;            // fp32 of 1 / (2 pi)
+constexpr float kInv2PiLo = 6.4206383e-09f;         // 1 / (2 pi) - kInv2PiHi
+template <int D>
+__device__ __forceinline__ void rope_pos_quad(const float *inv_freq, int ph, int pw, int i, f32x4 &c, f32x4 &s) {
+    constexpr int F = D / 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int col = 4 * i + e;
+        const bool isw = col >= F;
+        const float ang = (float)(isw ? pw : ph) * inv_freq[isw ? col - F : col];
+        const float hi = ang * kInv2PiHi;
+        const float lo = __builtin_fmaf(ang, kInv2PiHi, -hi) + ang * kInv2PiLo;
+        const float fr = __builtin_amdgcn_fractf(hi) + lo;
+        c[e] = __builtin_amdgcn_cosf(fr);
+        s[e] = __builtin_amdgcn_sinf(fr);
+    }
+}
+
+// load_rotate_quad (fra_device.h) with the angles of token `row` computed
+// from its position instead of read from cos/sin rows.
+template <int D, class E>
+__device__ __forceinline__ void load_rotate_quad_pos(const char *xrow, const KParams &p, int64_t row, int i,
+                                                     bool valid, u32x2 &r0w, u32x2 &r1w) {
+    u32x2 x0 = *(const u32x2 *)(xrow + 8 * i);
+    u32x2 x1 = *(const u32x2 *)(xrow + D + 8 * i);
+    const int2 hw = *(const int2 *)(p.pos + 2 * row);
+    f32x4 c, sn;
+    rope_pos_quad<D>(p.inv_freq, hw.x, hw.y, i, c, sn);
+    if (!valid) {
+        x0 = u32x2{0u, 0u};
+        x1 = u32x2{0u, 0u};
+    }
+    rotate_quad<E>(x0, x1, c, sn, c, sn, r0w, r1w);
+}
+
 // ---- window kernel ------------------------------------------------------------
 //
 // One workgroup of HW wavefronts per (segment, group of HW heads), HW = 2
@@ -224,8 +281,24 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
     // window's other head groups share nor leave dirty output lines in L2
     // for the end of the kernel to write back (measured: 1.6 us of 29 at a
     // 144-window layer).
-    f32x4 tv[TPER];
-    {
+    // The position variant loads each item's (h, w) instead (items (token,
+    // quad) of the cos and sin rows at once) and computes the quads below,
+    // while the Q and K slabs are still in flight.
+    constexpr bool POS = RD == kRopePos;
+    constexpr int PITEMS = 64 * TQ;
+    constexpr int PPER = (PITEMS + kWinThreads - 1) / kWinThreads;
+    f32x4 tv[POS ? 1 : TPER];
+    int2 tpos[POS ? PPER : 1];
+    f32x4 tvc[POS ? PPER : 1], tvs[POS ? PPER : 1];
+    if constexpr (POS) {
+        GridWalk<TQ, kWinThreads> it(fresh(tid));
+#pragma unroll
+        for (int k = 0; k < PPER; ++k) {
+            const int tok = min(it.row, 63);
+            tpos[k] = *(const int2 *)(p.pos + 2 * ((int64_t)s0 + (tok < L ? tok : 0)));
+            it.next();
+        }
+    } else {
         GridWalk<TN, kWinThreads> it(fresh(tid));
 #pragma unroll
         for (int k = 0; k < TPER; ++k) {
@@ -265,12 +338,32 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
         else load_slabs(BoolTag<false>{});
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (POS) {
+        GridWalk<TQ, kWinThreads> it(fresh(tid));
+#pragma unroll
+        for (int k = 0; k < PPER; ++k) {
+            rope_pos_quad<D>(p.inv_freq, tpos[k].x, tpos[k].y, it.col, tvc[k], tvs[k]);
+            it.next();
+        }
+    }
 
     // ---- 2. per half: tables and Q staged and rotated, then K ------------------------
     // Staging writes are branch-free (a branch here would make the compiler
     // wait for every outstanding load): items of the other half go to the
     // trash slot unless the half is known per item at compile time.
     auto stage_tab = [&](int hf) {
+        if constexpr (POS) {
+            GridWalk<TQ, kWinThreads> it(fresh(tid));
+#pragma unroll
+            for (int k = 0; k < PPER; ++k) {
+                const bool in = (PITEMS % kWinThreads == 0 || it.row < 64) && (it.row >> 5) == hf;
+                float *dst = tab + (it.row - 32 * hf) * CS + 4 * it.col;
+                *(f32x4 *)(in ? (char *)dst : trash) = tvc[k];
+                *(f32x4 *)(in ? (char *)(dst + W) : trash) = tvs[k];
+                it.next();
+            }
+            return;
+        }
         GridWalk<TN, kWinThreads> it(fresh(tid));
 #pragma unroll
         for (int k = 0; k < TPER; ++k) {
@@ -582,7 +675,7 @@ constexpr int long_vpitch(int need) {
 // krot_kernel once per call); the direct loads then fill the K_rot buffers
 // themselves and there is no raw staging or rotation in the loop.
 template <int D, int RD, bool FULL, bool PRE = false> struct LongLds {
-    static constexpr int RB = RD == FRA_DTYPE_F32 ? 4 : 2;
+    static constexpr int RB = Rope<RD>::kBytes;
     static constexpr int HALF = D / 2;
     static constexpr int W = FULL ? D : D / 2;         // table width
     static constexpr int DP = (D + 15) / 16 * 16;      // K_rot row padded to the MFMA k-step
@@ -629,9 +722,12 @@ __global__ __launch_bounds__(256) void krot_kernel(const KParams p) {
     const int i = (int)(it - row * NQ);
     const int t = (int)(row / p.num_heads), h = (int)(row - (int64_t)t * p.num_heads);
     u32x2 r0, r1;
-    load_rotate_quad<D, E, RD, FULL>(p.k + ((int64_t)t * p.sk_s + (int64_t)h * p.sk_h) * 2,
-                                     p.cos + (int64_t)t * p.sr_s * RB, p.sin + (int64_t)t * p.sr_s * RB, i, true,
-                                     r0, r1);
+    if constexpr (RD == kRopePos)
+        load_rotate_quad_pos<D, E>(p.k + ((int64_t)t * p.sk_s + (int64_t)h * p.sk_h) * 2, p, t, i, true, r0, r1);
+    else
+        load_rotate_quad<D, E, RD, FULL>(p.k + ((int64_t)t * p.sk_s + (int64_t)h * p.sk_h) * 2,
+                                         p.cos + (int64_t)t * p.sr_s * RB, p.sin + (int64_t)t * p.sr_s * RB, i, true,
+                                         r0, r1);
     char *dst = p.krot + row * (D * 2);
     *(u32x2 *)(dst + 8 * i) = r0;
     *(u32x2 *)(dst + 2 * HALF + 8 * i) = r1;
@@ -1020,8 +1116,10 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         const char *srow = p.sin + row * p.sr_s * RB;
         u32x2 nat[DP / 4];  // natural quads: 0..NQ-1 = x0r, NQ..2NQ-1 = x1r, rest 0
 #pragma unroll
-        for (int i = 0; i < NQ; ++i)
-            load_rotate_quad<D, E, RD, FULL>(qrow, crow, srow, i, valid, nat[i], nat[NQ + i]);
+        for (int i = 0; i < NQ; ++i) {
+            if constexpr (RD == kRopePos) load_rotate_quad_pos<D, E>(qrow, p, row, i, valid, nat[i], nat[NQ + i]);
+            else load_rotate_quad<D, E, RD, FULL>(qrow, crow, srow, i, valid, nat[i], nat[NQ + i]);
+        }
 #pragma unroll
         for (int i = 2 * NQ; i < DP / 4; ++i) nat[i] = u32x2{0u, 0u};
         // Bitwise select: a ?: on the two elements is folded into an index
@@ -1392,7 +1490,7 @@ namespace fra_internal {
 // The long kernel stages table rows as whole 16-byte chunks; 16-bit tables
 // whose rows are not (head_dim 72 at width head_dim/2) have no long kernel.
 template <int D, int RD, bool FULL> constexpr bool long_ok() {
-    return (FULL ? D : D / 2) * (RD == FRA_DTYPE_F32 ? 4 : 2) % 16 == 0;
+    return (FULL ? D : D / 2) * Rope<RD>::kBytes % 16 == 0;
 }
 
 template <int D, class E, int RD, bool FULL> void pick_full(bool window, int hw, Choice &c) {
@@ -1413,7 +1511,8 @@ template <int D, class E, int RD, bool FULL> void pick_full(bool window, int hw,
         }
     }
     if constexpr (long_ok<D, RD, FULL>()) {
-        c.fn = (KernelFn)long_kernel<D, E, RD, FULL, false>;
+        // (the position variant has no table rows to stage: rotated-K form only)
+        if constexpr (RD != kRopePos) c.fn = (KernelFn)long_kernel<D, E, RD, FULL, false>;
         c.merge = (KernelFn)split_merge_kernel<D, E>;
         c.lds = LongLds<D, RD, FULL>::kBytes;
         c.fn_pre = (KernelFn)long_kernel<D, E, RD, FULL, true>;
@@ -1427,7 +1526,20 @@ template <int D, class E, int RD> void pick_rd(bool window, int hw, bool full, C
     else pick_full<D, E, RD, false>(window, hw, c);
 }
 
+// The position variant: window kernels, and for long segments only the
+// rotated-K (workspace) form, whose K rotation computes the angles.
+template <int D, class E> void pick_pos(bool window, int hw, Choice &c) {
+    if constexpr (D % 4 == 0) {
+        pick_full<D, E, kRopePos, false>(window, hw, c);
+    }
+}
+
 template <int D> void pick_d(bool window, int hw, bool full, int qkv, int rd, Choice &c) {
+    if (rd == kRopePos) {
+        if (qkv == FRA_DTYPE_BF16) pick_pos<D, BF16>(window, hw, c);
+        else pick_pos<D, F16>(window, hw, c);
+        return;
+    }
     if (qkv == FRA_DTYPE_BF16) {
         if (rd == FRA_DTYPE_F32) pick_rd<D, BF16, FRA_DTYPE_F32>(window, hw, full, c);
         else if (rd == FRA_DTYPE_BF16) pick_rd<D, BF16, FRA_DTYPE_BF16>(window, hw, full, c);

@@ -38,7 +38,15 @@ struct KParams {
     float scale_log2;     // softmax_scale * log2(e)
     float *lse;           // optional [num_heads, total] natural-log row sums (NULL: not written)
     char *krot;           // long kernel, PRE variant: k_rot rows [total, num_heads, head_dim] (workspace)
+    // Rope from positions (fra_fwd_varlen_pos): (h, w) int32 per token and
+    // head_dim/4 inverse frequencies; cos/sin are then unused.
+    const int32_t *pos;
+    const float *inv_freq;
 };
+
+// Internal rope "dtype" of the position variant: the kernels compute cos/sin
+// from KParams::pos and ::inv_freq (table width head_dim / 2).
+constexpr int kRopePos = 3;
 
 typedef void (*KernelFn)(KParams);
 

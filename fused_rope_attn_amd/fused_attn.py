@@ -10,6 +10,10 @@ Drop-in for the reference module ``fused_attn.py``:
 * ``compute_rope_2d`` -- reference ``fused_attn.py:33-136`` (with its LRU
   cache, ``:18-30``): the cos/sin tables the op consumes.
 * ``next_pow2`` -- reference ``fused_attn.py:13-15``.
+* ``rope_positions_2d`` / ``fused_rope_attention_pos`` -- beyond the
+  reference: the same op with the rotation angles computed in the kernels
+  from each token's (h, w) patch position and the inverse frequencies, so
+  that no cos/sin table is built (``compute_rope_2d``) or read.
 
 Beyond the reference (which is forward-only): ``fused_rope_attention``
 records an autograd graph when q, k or v require grad, and
@@ -24,7 +28,8 @@ import torch
 from . import _lib
 
 __all__ = ["fused_rope_attention", "fused_rope_attention_fwd", "fused_rope_attention_bwd",
-           "compute_rope_2d", "next_pow2", "plan", "backward_plan"]
+           "compute_rope_2d", "next_pow2", "plan", "backward_plan",
+           "rope_positions_2d", "fused_rope_attention_pos", "plan_pos"]
 
 
 def next_pow2(n: int) -> int:
@@ -562,3 +567,177 @@ class _FusedRopeAttention(torch.autograd.Function):
         dv = torch.zeros(q.shape, dtype=q.dtype, device=q.device)
         _backward(dout, q, k, v, cos, sin, out, lse, cu, ctx.max_seqlen, ctx.scale, dq, dk, dv)
         return dq, dk, dv, None, None, None, None, None
+
+
+# ---------------------------------------------------------------------------
+# RoPE from positions (beyond the reference: compute_rope_2d's table is never
+# built; the kernels compute its angles, cosines and sines in registers)
+# ---------------------------------------------------------------------------
+
+def rope_positions_2d(grid_thw, head_dim: int, spatial_merge_size: int, theta: float, device,
+                      window_idx: "torch.Tensor | None" = None):
+    """``(pos, inv_freq)`` for ``fused_rope_attention_pos``: ``pos`` int32
+    ``[total_seq, 2]`` holds the (h, w) patch position of every row of
+    ``compute_rope_2d``'s tables (merge-block order, ``t`` repeats, the
+    ``window_idx`` reorder), ``inv_freq`` float32 ``[head_dim // 4]`` is
+    ``1/theta**(arange(0, D/2, 2)/(D/2))``.  Row t of the table is then
+    ``[pos[t, 0] * inv_freq || pos[t, 1] * inv_freq]`` (reference
+    fused_attn.py:78-116)."""
+    assert head_dim > 0 and head_dim % 4 == 0, f"head_dim must be divisible by 4, got {head_dim}"
+    rd = head_dim // 2
+    merge = int(spatial_merge_size)
+    device = torch.device(device)
+    if isinstance(grid_thw, torch.Tensor):
+        thw = [tuple(int(x) for x in row) for row in grid_thw.detach().cpu().tolist()]
+    else:
+        thw = [(int(t), int(h), int(w)) for t, h, w in grid_thw]
+    inv = 1.0 / (theta ** (torch.arange(0, rd, 2, device=device, dtype=torch.float32) / rd))
+    hs, ws = [], []
+    for t, h, w in thw:
+        hp, wp = _merge_order(h, w, merge, device)
+        hs.append(hp.repeat(t))
+        ws.append(wp.repeat(t))
+    pos = torch.stack([torch.cat(hs), torch.cat(ws)], dim=1).to(torch.int32)
+    if window_idx is not None:
+        mu = merge * merge
+        widx = window_idx.to(device=device, dtype=torch.long)
+        pos = pos.view(-1, mu, 2).index_select(0, widx).reshape(-1, 2)
+    return pos.contiguous(), inv.contiguous()
+
+
+def _validate_pos(q, k, v, pos, inv_freq, cu_seqlens, out) -> None:
+    """The op's checks with the tables replaced by positions."""
+    if q.device.type != "cuda":
+        raise ValueError(f"q must be on CUDA, got device={q.device}")
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError(f"q/k/v must have same shape, got q={tuple(q.shape)} k={tuple(k.shape)} v={tuple(v.shape)}")
+    if q.ndim != 3:
+        raise ValueError(f"q/k/v must be [total_seq, num_heads, head_dim], got q.ndim={q.ndim}")
+    total_seq, head_dim = int(q.shape[0]), int(q.shape[2])
+    if head_dim <= 0 or head_dim % 4 != 0:
+        raise ValueError(f"head_dim must be positive and divisible by 4 for rope positions, got {head_dim}")
+    if not _lib.load().fra_supports_head_dim(head_dim):
+        raise ValueError(f"head_dim={head_dim} has no kernel in this build of libfra.so (rope positions run "
+                         f"only at compiled head dims)")
+    if tuple(pos.shape) != (total_seq, 2):
+        raise ValueError(f"pos must be [total_seq, 2]={total_seq, 2}, got {tuple(pos.shape)}")
+    if pos.dtype.is_floating_point or pos.dtype.is_complex or pos.dtype == torch.bool:
+        raise ValueError(f"pos must have an integer dtype, got {pos.dtype}")
+    if tuple(inv_freq.shape) != (head_dim // 4,):
+        raise ValueError(f"inv_freq must be [head_dim//4]={head_dim // 4,}, got {tuple(inv_freq.shape)}")
+    if inv_freq.dtype != torch.float32:
+        raise ValueError(f"inv_freq must be float32, got {inv_freq.dtype}")
+    if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2:
+        raise ValueError(f"cu_seqlens must be 1D with length >= 2, got {tuple(cu_seqlens.shape)}")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"q dtype must be float16 or bfloat16, got {q.dtype}")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"q/k/v must share dtype, got q={q.dtype} k={k.dtype} v={v.dtype}")
+    if out is not None:
+        if out.shape != q.shape:
+            raise ValueError(f"out must have shape {tuple(q.shape)}, got {tuple(out.shape)}")
+        if out.dtype != q.dtype or out.device != q.device:
+            raise ValueError(f"out must match q dtype/device, got out={out.dtype}/{out.device} q={q.dtype}/{q.device}")
+    for name, t in (("k", k), ("v", v), ("pos", pos), ("inv_freq", inv_freq)):
+        if t.device != q.device:
+            raise ValueError(f"{name} must be on {q.device}, got {t.device}")
+
+
+def _pos_args(q, k, v, pos, inv_freq, out, cu, max_seqlen: int, scale: float):
+    """(FwdArgs, RopePositions, kept tensors) of one position call."""
+    qk, kk, vk = _prepare_qkv(q, k, v, _uses_long_kernel(max_seqlen, q.shape[2]))
+    pos = pos.to(dtype=torch.int32).contiguous()
+    inv_freq = inv_freq.contiguous()
+    a = _lib.FwdArgs()
+    a.q, a.k, a.v, a.out = qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr()
+    a.cos = a.sin = None
+    a.cu_seqlens = cu.data_ptr()
+    a.q_stride_seq, a.q_stride_head = qk.stride(0), qk.stride(1)
+    a.k_stride_seq, a.k_stride_head = kk.stride(0), kk.stride(1)
+    a.v_stride_seq, a.v_stride_head = vk.stride(0), vk.stride(1)
+    a.out_stride_seq, a.out_stride_head = out.stride(0), out.stride(1)
+    a.rope_stride_seq = 0
+    a.total_seq, a.num_heads, a.head_dim = q.shape
+    a.num_seqs = cu.numel() - 1
+    a.max_seqlen = int(max_seqlen)
+    a.rope_width = q.shape[2] // 2
+    a.qkv_dtype = _QKV_CODE[q.dtype]
+    a.rope_dtype = _lib.FRA_DTYPE_F32
+    a.softmax_scale = float(scale)
+    a.flags = 0
+    rope = _lib.RopePositions(pos.data_ptr(), inv_freq.data_ptr())
+    return a, rope, (qk, kk, vk, pos, inv_freq)
+
+
+def _prepare_qkv(q, k, v, long_kernel: bool):
+    q = _kernel_layout(q, 8, 4)
+    k = _kernel_layout(k, 16, 8) if long_kernel else _kernel_layout(k, 8, 4)
+    v = _kernel_layout(v, 16, 8)
+    return q, k, v
+
+
+def plan_pos(q, k, v, pos, inv_freq, cu_seqlens, max_seqlen: int, softmax_scale=None) -> dict:
+    """``plan`` of a ``fused_rope_attention_pos`` call (no launch)."""
+    cu = _prepare_cu(cu_seqlens, q.device)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    scale = q.shape[2] ** -0.5 if softmax_scale is None else softmax_scale
+    a, rope, _keep = _pos_args(q, k, v, pos, inv_freq, out, cu, max_seqlen, scale)
+    lib = _lib.load()
+    nbytes = ctypes.c_int64(0)
+    _lib.check(lib.fra_workspace_bytes_pos(a, rope, ctypes.byref(nbytes)))
+    a.workspace_bytes = int(nbytes.value)
+    pl = _lib.Plan()
+    _lib.check(lib.fra_query_plan_pos(a, rope, pl))
+    return {"kernel": {_lib.FRA_KERNEL_WINDOW: "window", _lib.FRA_KERNEL_LONG: "long"}.get(pl.kernel, "none"),
+            "name": pl.name.decode(), "grid": pl.grid, "block": pl.block, "lds_bytes": pl.lds_bytes,
+            "workspace_bytes": a.workspace_bytes, "split_units": pl.split_units, "split_parts": pl.split_parts}
+
+
+def fused_rope_attention_pos(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    pos: torch.Tensor,
+    inv_freq: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    max_seqlen: "int | None" = None,
+    softmax_scale: "float | None" = None,
+    *,
+    out: "torch.Tensor | None" = None,
+) -> torch.Tensor:
+    """``fused_rope_attention`` with the rotation computed from positions:
+    for token t, ``cos``/``sin`` row t of ``compute_rope_2d`` is evaluated in
+    the kernels as ``cos/sin([pos[t, 0] * inv_freq || pos[t, 1] *
+    inv_freq])`` (fp32 products, the device library's sincosf), so no table
+    is built or read.  ``pos`` and ``inv_freq`` come from
+    ``rope_positions_2d`` with the arguments ``compute_rope_2d`` would take.
+    Forward only; head_dim must be a multiple of 4 with its own kernels.
+    Returns ``out``."""
+    _validate_pos(q, k, v, pos, inv_freq, cu_seqlens, out)
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        raise RuntimeError("fused_rope_attention_pos() is forward only; use fused_rope_attention with "
+                           "compute_rope_2d tables for gradients")
+    cu = _prepare_cu(cu_seqlens, q.device)
+    if max_seqlen is None:
+        max_seqlen = int((cu[1:] - cu[:-1]).max().item())
+    max_seqlen = int(max_seqlen)
+    scale = q.shape[2] ** -0.5 if softmax_scale is None else float(softmax_scale)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if max_seqlen <= 0 or q.shape[0] == 0:
+        return out.zero_()
+    dst = out if _fits(out, 8, 4) else torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    a, rope, _keep = _pos_args(q, k, v, pos, inv_freq, dst, cu, max_seqlen, scale)
+    lib = _lib.load()
+    ws = None
+    with torch.cuda.device(q.device):
+        nbytes = ctypes.c_int64(0)
+        _lib.check(lib.fra_workspace_bytes_pos(a, rope, ctypes.byref(nbytes)))
+        if nbytes.value:
+            ws = torch.empty(int(nbytes.value), dtype=torch.uint8, device=q.device)
+            a.workspace, a.workspace_bytes = ws.data_ptr(), int(nbytes.value)
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        _lib.check(lib.fra_fwd_varlen_pos(a, rope, stream))
+    if dst is not out:
+        out.copy_(dst)
+    return out

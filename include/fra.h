@@ -168,6 +168,39 @@ int fra_fwd_varlen_static(const fra_fwd_args *args, void *stream);
 int fra_query_plan(const fra_fwd_args *args, fra_plan *plan);
 
 /*
+ * RoPE positions instead of cos/sin tables (fra_fwd_varlen_pos).  For token t
+ * with patch position (h, w) = (pos[2t], pos[2t + 1]) the kernels compute, in
+ * fp32, the angles of the reference's table row t (compute_rope_2d,
+ * fused_attn.py:78-116): column j < head_dim/4 is h * inv_freq[j], column
+ * head_dim/4 + j is w * inv_freq[j] (one fp32 product each, as the
+ * reference's outer product), and take their cosine and sine in registers.
+ * The table of width head_dim/2 is never materialised.
+ */
+typedef struct fra_rope_positions {
+    const int32_t *pos;         /* device, [total_seq, 2] contiguous int32 (h, w), rows in q/k order; 8-byte aligned */
+    const float *inv_freq;      /* device, [head_dim / 4] fp32: 1 / theta^(2j / (head_dim / 2)) */
+} fra_rope_positions;
+
+/*
+ * fra_fwd_varlen() with the rotation angles computed from positions
+ * (fra_rope_positions) instead of read from cos/sin tables.  Replaces the
+ * pair reference compute_rope_2d (fused_attn.py:33-136) + the table reads
+ * of the kernel (fused_attn.py:325-329, 370-374); the table is never built
+ * or read.  args->cos, args->sin, rope_width, rope_dtype and
+ * rope_stride_seq are ignored (cos/sin may be NULL); head_dim must be a
+ * multiple of 4.  Segments longer than 64 tokens need the rotated-K part of
+ * a workspace (fra_workspace_bytes() of the same args): the long kernel
+ * takes K rotated once per call; without it the call returns
+ * FRA_EUNSUPPORTED.  Forward only (fra_bwd_varlen takes tables).
+ */
+int fra_fwd_varlen_pos(const fra_fwd_args *args, const fra_rope_positions *rope, void *stream);
+
+/* fra_workspace_bytes() and fra_query_plan() of a fra_fwd_varlen_pos() call
+ * (no counterpart in the reference, which has no position variant). */
+int fra_workspace_bytes_pos(const fra_fwd_args *args, const fra_rope_positions *rope, int64_t *bytes);
+int fra_query_plan_pos(const fra_fwd_args *args, const fra_rope_positions *rope, fra_plan *plan);
+
+/*
  * Workspace bytes the long kernel can use for these arguments (their
  * workspace fields are ignored): rotated K plus the split scratch when a
  * split applies; 0 for the window kernel.  No counterpart in
