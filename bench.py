@@ -39,7 +39,8 @@ if ROOT not in sys.path:
 from fused_rope_attn_amd import (fused_rope_attention, fused_rope_attention_bwd,  # noqa: E402
                                  fused_rope_attention_fwd, fused_rope_attention_pos, plan, plan_pos)
 from fused_rope_attn_amd.configs import (WORKLOADS, algorithmic_bytes, algorithmic_bytes_bwd,  # noqa: E402
-                                         algorithmic_flops, algorithmic_flops_bwd, make_inputs, positions)
+                                         algorithmic_flops, algorithmic_flops_bwd, image_order, make_inputs,
+                                         positions)
 
 METRIC = "µs/call fused RoPE+varlen attn (1344² window layer); % HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
@@ -344,6 +345,55 @@ def run_positions(name: str, steps: int, warmup: int, flush: torch.Tensor, dev) 
             "max_abs_diff": float((ref.float() - got.float()).abs().max())}
 
 
+HIDDEN = 1280  # Qwen2.5-VL vision hidden size: the encoder shuffles [N, HIDDEN] hidden states
+
+
+def run_gather(name: str, steps: int, warmup: int, flush: torch.Tensor, dev) -> dict:
+    """A window layer on window-ordered tensors (the reference's route) and
+    on image-ordered tensors through ``row_index`` (the shuffle fused into
+    the kernel's addressing), timed alternately, beside the two gathers the
+    fused form removes from an encoder pass: ``window_shuffle`` of the
+    ``[N, 1280]`` bf16 hidden state before the blocks and
+    ``window_unshuffle`` after them."""
+    from fused_rope_attn_amd import window_shuffle, window_unshuffle, get_window_index
+    w = WORKLOADS[name]
+    inp = make_inputs(w, seed=1234 + list(WORKLOADS).index(name), device=dev)
+    rows, cos_i, sin_i = image_order(w, dev)
+    inv = torch.empty_like(rows, dtype=torch.int64)
+    inv[rows.long()] = torch.arange(rows.numel(), device=dev)
+    q, k, v, cos, sin, cu = (inp[x] for x in ("q", "k", "v", "cos", "sin", "cu_seqlens"))
+    qi, ki, vi = q[inv], k[inv], v[inv]
+    ms = inp["max_seqlen"]
+    out, outi = torch.empty_like(q), torch.empty_like(q)
+
+    def win():
+        fused_rope_attention(q, k, v, cos, sin, cu, ms, out=out)
+
+    def gat():
+        fused_rope_attention(qi, ki, vi, cos_i, sin_i, cu, ms, out=outi, row_index=rows)
+
+    hid = torch.randn(rows.numel(), HIDDEN, device=dev).to(torch.bfloat16)
+    widx = rows.view(-1, 4)[:, 0].long() // 4 if len(w.groups) == 1 and w.groups[0][1] == 2 else None
+
+    a1 = time_calls(win, steps, warmup, flush)
+    g1 = time_calls(gat, steps, warmup, flush)
+    a2 = time_calls(win, steps, warmup, flush)
+    g2 = time_calls(gat, steps, warmup, flush)
+    row = {"workload": name, "note": w.note,
+           "window_order_cold_us": (a1["cold_median_us"] + a2["cold_median_us"]) / 2,
+           "image_order_gather_cold_us": (g1["cold_median_us"] + g2["cold_median_us"]) / 2}
+    row["gather_over_window_order"] = row["image_order_gather_cold_us"] / row["window_order_cold_us"]
+    if widx is not None:
+        sh = time_calls(lambda: window_shuffle(hid, widx), steps, warmup, flush)
+        un = time_calls(lambda: window_unshuffle(hid, widx), steps, warmup, flush)
+        row["hidden_shuffle_cold_us"] = sh["cold_median_us"]
+        row["hidden_unshuffle_cold_us"] = un["cold_median_us"]
+        row["window_layers_to_break_even"] = ((sh["cold_median_us"] + un["cold_median_us"])
+                                              / max(1e-9, row["image_order_gather_cold_us"]
+                                                    - row["window_order_cold_us"]))
+    return row
+
+
 def run_backward(name: str, steps: int, warmup: int, flush: torch.Tensor, dev) -> dict:
     w = WORKLOADS[name]
     inp = make_inputs(w, seed=1234 + list(WORKLOADS).index(name), device=dev)
@@ -598,6 +648,10 @@ def main() -> int:
                     help="time the position variant (fused_rope_attention_pos) beside the table op for every "
                          "workload and write them to FILE")
     ap.add_argument("--pos", action="store_true", help="profiling driver: run the position variant instead")
+    ap.add_argument("--gather", default=None, metavar="FILE",
+                    help="time window layers in image order through row_index (the window shuffle fused into the "
+                         "kernel) beside the window-ordered call and the two hidden-state shuffles it removes; "
+                         "write them to FILE")
     ap.add_argument("--drift", default=None, metavar="FILE",
                     help="run the 32-layer drift stack on --workload's grid and write the report to FILE")
     args = ap.parse_args()
@@ -633,6 +687,16 @@ def main() -> int:
                   f"{r['positions_cold_us']:.1f} us ({r['positions_over_tables']:.3f}x), max-abs diff "
                   f"{r['max_abs_diff']:.2e}", file=sys.stderr, flush=True)
         with open(args.positions, "w") as f:
+            json.dump(rows, f, indent=1)
+        return 0
+    if args.gather:
+        rows = []
+        for name in ("cfg0", "cfg1", "cfg2w", "cfg3"):
+            r = run_gather(name, max(10, args.steps // 2), max(3, args.warmup // 2), flush, dev)
+            rows.append(r)
+            print(f"[bench] gather {name}: " + ", ".join(f"{k} {v:.4g}" for k, v in r.items()
+                                                        if isinstance(v, float)), file=sys.stderr, flush=True)
+        with open(args.gather, "w") as f:
             json.dump(rows, f, indent=1)
         return 0
     if args.backward:

@@ -108,6 +108,8 @@ SIGNATURES = {
     "fra_fwd_varlen_static": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.c_void_p]),
     "fra_query_plan": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(Plan)]),
     "fra_fwd_varlen_pos": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(RopePositions), ctypes.c_void_p]),
+    "fra_fwd_varlen_gather": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(RopePositions), ctypes.c_void_p,
+                                             ctypes.c_void_p]),
     "fra_workspace_bytes_pos": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(RopePositions),
                                                ctypes.POINTER(ctypes.c_int64)]),
     "fra_query_plan_pos": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.POINTER(RopePositions),

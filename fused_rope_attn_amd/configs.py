@@ -27,7 +27,7 @@ from .fused_attn import compute_rope_2d
 from .utils import get_window_index
 
 __all__ = ["Workload", "WORKLOADS", "make_inputs", "algorithmic_bytes", "algorithmic_flops",
-           "algorithmic_bytes_bwd", "algorithmic_flops_bwd", "positions"]
+           "algorithmic_bytes_bwd", "algorithmic_flops_bwd", "positions", "image_order"]
 
 
 @dataclass(frozen=True)
@@ -97,6 +97,27 @@ def positions(w: Workload, device="cpu"):
         pos, inv = rope_positions_2d(grids, w.head_dim, merge, w.theta, "cpu", window_idx=widx)
         poss.append(pos)
     return torch.cat(poss).to(device), inv.to(device)
+
+
+def image_order(w: Workload, device="cpu", rope_dtype=torch.float32):
+    """``(row_index int32 [N], cos, sin)`` of a window workload kept in image
+    order: ``layout``'s tables without the window reorder, and the row of
+    every window-order slot (``utils.window_row_index``, offset per image
+    group), so that ``x_window = x_image[row_index]`` for every tensor."""
+    from .utils import window_row_index
+    assert w.kind == "window", w.kind
+    rows, coss, sins = [], [], []
+    offset = 0
+    for grids, merge in w.groups:
+        grids = [tuple(g) for g in grids]
+        widx, cu = get_window_index(grids, window_size=w.window_size, spatial_merge_size=merge,
+                                    patch_size=w.patch_size, device="cpu")
+        cos, sin = compute_rope_2d(grids, w.head_dim, merge, w.theta, "cpu", rope_dtype)
+        rows.append(window_row_index(widx, spatial_merge_size=merge) + offset)
+        offset += int(cu[-1])
+        coss.append(cos)
+        sins.append(sin)
+    return torch.cat(rows).to(device), torch.cat(coss).to(device), torch.cat(sins).to(device)
 
 
 def make_inputs(w: Workload, seed: int = 0, device="cpu", dtype=torch.bfloat16, rope_dtype=torch.float32,

@@ -94,8 +94,10 @@ const char *dtype_name(int dt) {
 // rotated in the long kernel); all of the workspace may hold split scratch.
 // rope non-NULL: the position variant (fra_fwd_varlen_pos); the cos/sin
 // fields of args are then ignored.
+// rows non-NULL: the row-gather variant (fra_fwd_varlen_gather), window
+// layers only.
 int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true,
-         const fra_rope_positions *rope = nullptr) {
+         const fra_rope_positions *rope = nullptr, const int32_t *rows = nullptr) {
     if (!a) return fail(FRA_EINVAL, "args is NULL");
     if (a->flags != 0) return fail(FRA_EINVAL, "flags must be 0, got %d", a->flags);
     if (a->num_heads <= 0) return fail(FRA_EINVAL, "num_heads must be positive, got %d", a->num_heads);
@@ -136,7 +138,13 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true,
     const int64_t max_row_bytes = 2 * std::max(std::max(a->q_stride_seq, a->k_stride_seq),
                                                std::max(a->v_stride_seq, a->out_stride_seq));
     const bool small_rows = 64 * max_row_bytes < ((int64_t)1 << 31) && 64 * 4 * rope_stride < ((int64_t)1 << 31);
-    const bool window = a->max_seqlen <= 64 && d <= kWindowMaxD && small_rows;
+    // (the gather variant addresses its rows with 64-bit offsets)
+    const bool window = a->max_seqlen <= 64 && d <= kWindowMaxD && (small_rows || rows);
+    if (rows && !window)
+        return fail(FRA_EUNSUPPORTED,
+                    "the row gather is for window layers: segments of at most 64 tokens at head_dim <= %d "
+                    "(max_seqlen %d, head_dim %d)", kWindowMaxD, a->max_seqlen, d);
+    if (rows && !aligned(rows, 4)) return fail(FRA_EINVAL, "row_index must be 4-byte aligned");
     memset(&c, 0, sizeof(c));
     if (!pick_kernel(d, window, kWinHeadsMax, full, a->qkv_dtype, rd, c))
         return fail(FRA_EUNSUPPORTED, "head_dim=%d has no compiled kernel (built:" FRA_HEAD_DIMS_STRING ")", d);
@@ -193,6 +201,7 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true,
     kp.sr_s = rope_stride;
     kp.pos = pos ? rope->pos : nullptr;
     kp.inv_freq = pos ? rope->inv_freq : nullptr;
+    kp.rows = rows;
     kp.total = a->total_seq;
     kp.num_heads = a->num_heads;
     kp.num_seqs = a->num_seqs;
@@ -226,7 +235,9 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true,
         c.block = 64 * c.heads;
         c.block_q = 64;
         c.block_kv = 64;
-        snprintf(c.name, sizeof(c.name), "window_d%d_%s_rope%s", d, dtype_name(a->qkv_dtype), dtype_name(rd));
+        snprintf(c.name, sizeof(c.name), "window_d%d_%s_rope%s%s", d, dtype_name(a->qkv_dtype), dtype_name(rd),
+                 rows ? "_gather" : "");
+        if (rows) c.fn = c.fn_gather;
     } else {
         kp.qblocks = (a->max_seqlen + kLongBQ - 1) / kLongBQ;
         const int64_t units = sh * kp.qblocks;
@@ -379,6 +390,16 @@ int fra_fwd_varlen_static(const fra_fwd_args *args, void *stream) {
         }
     }
     return launch(&a, c, kp, stream);
+}
+
+int fra_fwd_varlen_gather(const fra_fwd_args *args, const fra_rope_positions *rope, const int32_t *row_index,
+                          void *stream) {
+    if (!row_index) return fail(FRA_EINVAL, "row_index is NULL");
+    Choice c;
+    KParams kp;
+    const int rc = plan(args, c, kp, true, rope, row_index);
+    if (rc != FRA_OK) return rc;
+    return launch(args, c, kp, stream);
 }
 
 int fra_fwd_varlen_pos(const fra_fwd_args *args, const fra_rope_positions *rope, void *stream) {

@@ -205,7 +205,7 @@ template <int D, bool FULL, int HW> struct WinLds {
     static constexpr int kPerCu = (160 * 1024 / kBytes) < (4 * kWaves / HW) ? (160 * 1024 / kBytes) : (4 * kWaves / HW);
 };
 
-template <int D, class E, int RD, bool FULL, int HW>
+template <int D, class E, int RD, bool FULL, int HW, bool GATHER>
 __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window_kernel(const KParams p) {
     using LDS = WinLds<D, FULL, HW>;
     constexpr int kWinHeads = HW;
@@ -266,7 +266,14 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
     // Full window, four heads, each token's heads adjacent in every tensor:
     // chunk c of slab row t is at t * row_stride + 16 c, and row offsets are
     // stepped instead of multiplied.
-    const bool fast = p.dense_heads && nh == kWinHeads && L == 64;  // uniform
+    const bool fast = !GATHER && p.dense_heads && nh == kWinHeads && L == 64;  // uniform
+    // GATHER (fra_fwd_varlen_gather): slot s0 + t of the window is tensor row
+    // p.rows[s0 + t] (clamped into the tensors), for every tensor and table;
+    // byte offset of that row from row s0 at row stride rs.
+    auto grow_bytes = [&](int t, uint32_t rs) -> int64_t {
+        const int rr = min(max(p.rows[s0 + t], 0), p.total - 1);
+        return (int64_t)(rr - s0) * rs;
+    };
     // Byte offset of chunk `col` of a slab row: head col / HCH (heads past
     // the group's last read its first), chunk col % HCH.
     auto chunk_off = [&](int col, uint32_t hs) {
@@ -295,7 +302,9 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
 #pragma unroll
         for (int k = 0; k < PPER; ++k) {
             const int tok = min(it.row, 63);
-            tpos[k] = *(const int2 *)(p.pos + 2 * ((int64_t)s0 + (tok < L ? tok : 0)));
+            const int tt = tok < L ? tok : 0;
+            if constexpr (GATHER) tpos[k] = *(const int2 *)(p.pos + 2 * ((int64_t)s0 + grow_bytes(tt, 1)));
+            else tpos[k] = *(const int2 *)(p.pos + 2 * ((int64_t)s0 + tt));
             it.next();
         }
     } else {
@@ -304,8 +313,13 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
         for (int k = 0; k < TPER; ++k) {
             const int tok = min(it.row, 63), c = it.col;
             const bool is_sin = c >= TQ;
-            const uint32_t off = (uint32_t)(tok < L ? tok : 0) * trs + (uint32_t)(4 * RB * (is_sin ? c - TQ : c));
-            tv[k] = Rope<RD>::quad((is_sin ? sb : cb) + off);
+            const uint32_t qoff = (uint32_t)(4 * RB * (is_sin ? c - TQ : c));
+            if constexpr (GATHER) {
+                tv[k] = Rope<RD>::quad((is_sin ? sb : cb) + grow_bytes(tok < L ? tok : 0, trs) + qoff);
+            } else {
+                const uint32_t off = (uint32_t)(tok < L ? tok : 0) * trs + qoff;
+                tv[k] = Rope<RD>::quad((is_sin ? sb : cb) + off);
+            }
             it.next();
         }
     }
@@ -322,6 +336,10 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
                 if constexpr (F) {
                     qs[k] = __builtin_nontemporal_load((const u32x4 *)(qb + (qro + 16 * it.col)));
                     ks[k] = __builtin_nontemporal_load((const u32x4 *)(kb + (kro + 16 * it.col)));
+                } else if constexpr (GATHER) {
+                    const int row = it.row < L ? it.row : 0;
+                    qs[k] = __builtin_nontemporal_load((const u32x4 *)(qb + grow_bytes(row, qrs) + chunk_off(it.col, qhs)));
+                    ks[k] = __builtin_nontemporal_load((const u32x4 *)(kb + grow_bytes(row, krs) + chunk_off(it.col, khs)));
                 } else {
                     const uint32_t row = it.row < L ? (uint32_t)it.row : 0u;
                     qs[k] = __builtin_nontemporal_load((const u32x4 *)(qb + (row * qrs + chunk_off(it.col, qhs))));
@@ -448,10 +466,11 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
                 const int m = w + kWinHeads * k;
                 if (VPC % kWinHeads == 0 || m < VPC) {  // uniform
                     if (it.col < NCH) {
-                        uint32_t off;
-                        if constexpr (F) off = vro + 16 * it.col;
-                        else off = (uint32_t)min(it.row, L - 1) * vrs + chunk_off(it.col, vhs);
-                        __builtin_amdgcn_global_load_lds((glb_void *)(vb + off), (lds_void *)(lds + 1024 * m), 16, 0, 0);
+                        const char *src;
+                        if constexpr (F) src = vb + (vro + 16 * it.col);
+                        else if constexpr (GATHER) src = vb + grow_bytes(min(it.row, L - 1), vrs) + chunk_off(it.col, vhs);
+                        else src = vb + ((uint32_t)min(it.row, L - 1) * vrs + chunk_off(it.col, vhs));
+                        __builtin_amdgcn_global_load_lds((glb_void *)src, (lds_void *)(lds + 1024 * m), 16, 0, 0);
                     }
                 }
                 const bool cy = it.next();
@@ -530,7 +549,8 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
         lsum = sum_pair32(lsum);
         const float inv = 1.0f / lsum;
         if (p.lse != nullptr && g == 0 && 32 * b + r < L)
-            p.lse[(int64_t)(h0 + w) * p.total + s0 + 32 * b + r] = (__builtin_amdgcn_logf(lsum) - mneg) * kLn2;
+            p.lse[(int64_t)(h0 + w) * p.total + s0 + (GATHER ? grow_bytes(32 * b + r, 1) : 32 * b + r)] =
+                (__builtin_amdgcn_logf(lsum) - mneg) * kLn2;
 
         // P^T as the B operand of O^T = V^T P^T: step (a, h) uses elements
         // 8h..8h+7 of sacc[a], i.e. kv = 32a + 16h + {4g..4g+3, 8+4g..8+4g+3}.
@@ -604,7 +624,10 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
                 if constexpr (F) {
                     __builtin_nontemporal_store(val, (u32x4 *)(ob + (oro + 16 * it.col)));
                 } else if (it.row < L && it.col < nh * HCH) {
-                    __builtin_nontemporal_store(val, (u32x4 *)(ob + ((uint32_t)it.row * ors + chunk_off(it.col, ohs))));
+                    if constexpr (GATHER)
+                        __builtin_nontemporal_store(val, (u32x4 *)(ob + grow_bytes(it.row, ors) + chunk_off(it.col, ohs)));
+                    else
+                        __builtin_nontemporal_store(val, (u32x4 *)(ob + ((uint32_t)it.row * ors + chunk_off(it.col, ohs))));
                 }
                 const bool cy = it.next();
                 if constexpr (F) oro += GridWalk<NCH, kWinThreads>::Q * ors + (cy ? ors : 0u);
@@ -1498,11 +1521,13 @@ template <int D, class E, int RD, bool FULL> void pick_full(bool window, int hw,
     if constexpr (D <= kWindowMaxD) {
         if (window) {
             if (hw == 2) {
-                c.fn = (KernelFn)window_kernel<D, E, RD, FULL, 2>;
+                c.fn = (KernelFn)window_kernel<D, E, RD, FULL, 2, false>;
+                c.fn_gather = (KernelFn)window_kernel<D, E, RD, FULL, 2, true>;
                 c.lds = WinLds<D, FULL, 2>::kBytes;
                 c.per_cu = WinLds<D, FULL, 2>::kPerCu;
             } else {
-                c.fn = (KernelFn)window_kernel<D, E, RD, FULL, 4>;
+                c.fn = (KernelFn)window_kernel<D, E, RD, FULL, 4, false>;
+                c.fn_gather = (KernelFn)window_kernel<D, E, RD, FULL, 4, true>;
                 c.lds = WinLds<D, FULL, 4>::kBytes;
                 c.per_cu = WinLds<D, FULL, 4>::kPerCu;
             }

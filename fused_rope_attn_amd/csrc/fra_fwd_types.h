@@ -42,6 +42,9 @@ struct KParams {
     // head_dim/4 inverse frequencies; cos/sin are then unused.
     const int32_t *pos;
     const float *inv_freq;
+    // Window kernel, gather variant (fra_fwd_varlen_gather): tensor row of
+    // every slot of cu_seqlens' index space (NULL: the slot itself).
+    const int32_t *rows;
 };
 
 // Internal rope "dtype" of the position variant: the kernels compute cos/sin
@@ -81,6 +84,7 @@ struct Choice {
     KernelFn merge;   // split_merge_kernel of the long kernel's instance
     KernelFn fn_pre;  // long kernel, PRE variant (K rotated beforehand by krot)
     KernelFn krot;    // krot_kernel of the instance
+    KernelFn fn_gather;  // window kernel: the row-gather instance
     int lds_pre;
     int pre;          // the plan uses fn_pre and krot
     int kernel, grid, block, block_q, block_kv, lds, split_units, split_parts;

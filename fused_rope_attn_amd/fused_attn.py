@@ -341,6 +341,7 @@ def fused_rope_attention(
     softmax_scale: "float | None" = None,
     *,
     out: "torch.Tensor | None" = None,
+    row_index: "torch.Tensor | None" = None,
 ) -> torch.Tensor:
     """Fused split-half RoPE on Q and K + non-causal attention over packed
     segments (reference fused_attn.py:139-232).
@@ -358,11 +359,18 @@ def fused_rope_attention(
         the call free of host synchronisation (graph-capturable).
       - softmax_scale: defaults to ``head_dim ** -0.5``.
       - out: optional ``[total_seq, num_heads, head_dim]`` result buffer.
+      - row_index: optional ``[total_seq]`` integer tensor (beyond the
+        reference): the window shuffle fused into the kernel's addressing.
+        q, k, v, cos, sin and out stay in image order; ``cu_seqlens``
+        describes the windows over window-order slots and slot i uses row
+        ``row_index[i]`` (``utils.window_row_index``).  Window layers only
+        (segments of at most 64 tokens, head_dim <= 96); forward only.
 
     Rows outside every segment are left unwritten, as in the reference.
     Returns ``out``.
     """
     _validate(q, k, v, cos, sin, cu_seqlens, out)
+    rows = _prepare_rows(row_index, q)
     cu = _prepare_cu(cu_seqlens, q.device)
     if max_seqlen is None:
         max_seqlen = int((cu[1:] - cu[:-1]).max().item())
@@ -372,15 +380,29 @@ def fused_rope_attention(
         if out is not None:
             raise RuntimeError("fused_rope_attention(): out= does not support automatic differentiation "
                                "(q, k or v requires grad)")
+        if rows is not None:
+            raise RuntimeError("fused_rope_attention(): row_index is forward only (q, k or v requires grad)")
         return _FusedRopeAttention.apply(q, k, v, cos, sin, cu, max_seqlen, scale)
     if out is None:
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    return _forward(q, k, v, cos, sin, cu, max_seqlen, scale, out, None)
+    return _forward(q, k, v, cos, sin, cu, max_seqlen, scale, out, None, rows)
 
 
-def _forward(q, k, v, cos, sin, cu, max_seqlen: int, scale: float, out, lse):
+def _prepare_rows(row_index, q):
+    """``row_index`` as contiguous int32 on q's device (None stays None)."""
+    if row_index is None:
+        return None
+    if row_index.ndim != 1 or row_index.numel() != q.shape[0]:
+        raise ValueError(f"row_index must be [total_seq]={q.shape[0],}, got {tuple(row_index.shape)}")
+    if row_index.dtype.is_floating_point or row_index.dtype.is_complex or row_index.dtype == torch.bool:
+        raise ValueError(f"row_index must have an integer dtype, got {row_index.dtype}")
+    return row_index.to(device=q.device, dtype=torch.int32).contiguous()
+
+
+def _forward(q, k, v, cos, sin, cu, max_seqlen: int, scale: float, out, lse, rows=None):
     """One forward launch into ``out`` (and ``lse`` if given, [heads, tokens]
-    fp32); inputs already validated, ``cu`` int32 on q's device."""
+    fp32); inputs already validated, ``cu`` int32 on q's device; ``rows``
+    the optional int32 row gather."""
     if max_seqlen <= 0 or q.shape[0] == 0:
         if lse is not None:
             lse.fill_(float("-inf"))
@@ -392,8 +414,11 @@ def _forward(q, k, v, cos, sin, cu, max_seqlen: int, scale: float, out, lse):
         # every segment come back unchanged.
         outp = _pad_tail(out, d, dp)
         _forward(_pad_halves(q, d, dp), _pad_halves(k, d, dp), _pad_tail(v, d, dp), _pad_table(cos, d, dp),
-                 _pad_table(sin, d, dp), cu, max_seqlen, scale, outp, lse)
+                 _pad_table(sin, d, dp), cu, max_seqlen, scale, outp, lse, rows)
         return out.copy_(outp[..., :d])
+    if rows is not None and _uses_long_kernel(max_seqlen, d):
+        raise ValueError(f"row_index is for window layers (segments of at most 64 tokens, head_dim <= 96), "
+                         f"got max_seqlen={max_seqlen}, head_dim={d}")
     qk, kk, vk, cosk, sink = _prepare(q, k, v, cos, sin, _uses_long_kernel(max_seqlen, q.shape[2]))
     dst = out if _fits(out, 8, 4) else torch.empty(q.shape, dtype=q.dtype, device=q.device)
 
@@ -413,7 +438,10 @@ def _forward(q, k, v, cos, sin, cu, max_seqlen: int, scale: float, out, lse):
             ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
             args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        _lib.check(lib.fra_fwd_varlen(args, stream))
+        if rows is not None:
+            _lib.check(lib.fra_fwd_varlen_gather(args, None, rows.data_ptr(), stream))
+        else:
+            _lib.check(lib.fra_fwd_varlen(args, stream))
     if dst is not out:
         out.copy_(dst)
     return out
@@ -704,6 +732,7 @@ def fused_rope_attention_pos(
     softmax_scale: "float | None" = None,
     *,
     out: "torch.Tensor | None" = None,
+    row_index: "torch.Tensor | None" = None,
 ) -> torch.Tensor:
     """``fused_rope_attention`` with the rotation computed from positions:
     for token t, ``cos``/``sin`` row t of ``compute_rope_2d`` is evaluated in
@@ -712,8 +741,10 @@ def fused_rope_attention_pos(
     is built or read.  ``pos`` and ``inv_freq`` come from
     ``rope_positions_2d`` with the arguments ``compute_rope_2d`` would take.
     Forward only; head_dim must be a multiple of 4 with its own kernels.
-    Returns ``out``."""
+    ``row_index`` as in ``fused_rope_attention`` (``pos`` then in image
+    order too).  Returns ``out``."""
     _validate_pos(q, k, v, pos, inv_freq, cu_seqlens, out)
+    rows = _prepare_rows(row_index, q)
     if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
         raise RuntimeError("fused_rope_attention_pos() is forward only; use fused_rope_attention with "
                            "compute_rope_2d tables for gradients")
@@ -737,7 +768,13 @@ def fused_rope_attention_pos(
             ws = torch.empty(int(nbytes.value), dtype=torch.uint8, device=q.device)
             a.workspace, a.workspace_bytes = ws.data_ptr(), int(nbytes.value)
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        _lib.check(lib.fra_fwd_varlen_pos(a, rope, stream))
+        if rows is not None:
+            if _uses_long_kernel(max_seqlen, q.shape[2]):
+                raise ValueError(f"row_index is for window layers (segments of at most 64 tokens, head_dim <= "
+                                 f"96), got max_seqlen={max_seqlen}, head_dim={q.shape[2]}")
+            _lib.check(lib.fra_fwd_varlen_gather(a, rope, rows.data_ptr(), stream))
+        else:
+            _lib.check(lib.fra_fwd_varlen_pos(a, rope, stream))
     if dst is not out:
         out.copy_(dst)
     return out

@@ -114,3 +114,18 @@ def window_unshuffle(x: torch.Tensor, window_index: torch.Tensor, *, spatial_mer
     inv = torch.empty_like(idx)
     inv[idx] = torch.arange(idx.numel(), device=idx.device, dtype=idx.dtype)
     return x.reshape(n // mu, mu, *x.shape[1:]).index_select(0, inv).reshape(x.shape)
+
+
+def window_row_index(window_index: torch.Tensor, *, spatial_merge_size: int = 2) -> torch.Tensor:
+    """The token-level gather of ``window_shuffle`` as an int32 index:
+    ``window_shuffle(x)[i] == x[row[i]]`` with ``row[i] =
+    window_index[i // m^2] * m^2 + i % m^2`` (reference utils.py:105-126).
+    Passed as ``row_index`` to ``fused_rope_attention``, it lets a window
+    layer run on tensors kept in image order (no shuffle before the encoder
+    blocks, no unshuffle after)."""
+    mu = int(spatial_merge_size) ** 2
+    if mu <= 0:
+        raise ValueError(f"spatial_merge_size must be > 0, got {spatial_merge_size}")
+    idx = window_index.to(dtype=torch.int64)
+    rows = idx[:, None] * mu + torch.arange(mu, device=idx.device, dtype=torch.int64)[None, :]
+    return rows.reshape(-1).to(torch.int32)

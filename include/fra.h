@@ -195,6 +195,25 @@ typedef struct fra_rope_positions {
  */
 int fra_fwd_varlen_pos(const fra_fwd_args *args, const fra_rope_positions *rope, void *stream);
 
+/*
+ * The window shuffle fused into the kernel's addressing: a window layer on
+ * tensors kept in image order.  cu_seqlens describes the windows over the
+ * slots 0 .. total_seq-1 of window order, as for fra_fwd_varlen(), and slot
+ * i reads and writes row row_index[i] of q, k, v, out and of cos/sin (or
+ * pos) -- the gather reference window_shuffle does before the encoder's
+ * blocks (utils.py:105-126: row_index[i] = window_index[i / m^2] * m^2 +
+ * i % m^2) and whose inverse window_unshuffle applies after them
+ * (utils.py:129-153).  lse, when given, is indexed by tensor row.  Rows
+ * that no segment's slot maps to are not written.  row_index is device
+ * int32 [total_seq], 4-byte aligned; entries are clamped into [0, total_seq).
+ * rope NULL: tables from args (as fra_fwd_varlen); else positions (as
+ * fra_fwd_varlen_pos).  Window layers only (segments of at most 64 tokens,
+ * head_dim <= 96); otherwise FRA_EUNSUPPORTED.  No counterpart in the
+ * reference, which shuffles with two gathers around the encoder.
+ */
+int fra_fwd_varlen_gather(const fra_fwd_args *args, const fra_rope_positions *rope, const int32_t *row_index,
+                          void *stream);
+
 /* fra_workspace_bytes() and fra_query_plan() of a fra_fwd_varlen_pos() call
  * (no counterpart in the reference, which has no position variant). */
 int fra_workspace_bytes_pos(const fra_fwd_args *args, const fra_rope_positions *rope, int64_t *bytes);

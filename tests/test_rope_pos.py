@@ -109,3 +109,19 @@ def test_pos_validation():
     assert lib.fra_fwd_varlen_pos(_args(), _lib.RopePositions((1 << 24) + 4, 1 << 25), None) == _lib.FRA_EUNSUPPORTED
     # cos/sin stay NULL for the position variant, but the table entry point needs them
     assert lib.fra_fwd_varlen(_args(), None) == _lib.FRA_EINVAL
+
+
+def test_gather_plan_and_validation():
+    lib = _lib.load()
+    a = _args()
+    a.cos, a.sin, a.rope_stride_seq = 1 << 24, 1 << 24, 40
+    # long segments: no gather variant
+    a.max_seqlen, a.num_seqs = 9216, 1
+    rc = lib.fra_fwd_varlen_gather(a, None, 1 << 27, None)
+    assert rc == _lib.FRA_EUNSUPPORTED and "window layers" in _lib.last_error()
+    a.max_seqlen, a.num_seqs = 64, 144
+    assert lib.fra_fwd_varlen_gather(a, None, None, None) == _lib.FRA_EINVAL
+    assert lib.fra_fwd_varlen_gather(a, None, (1 << 27) + 2, None) == _lib.FRA_EINVAL  # alignment
+    a.total_seq = 0  # nothing to launch: a valid plan returns OK without touching the GPU
+    assert lib.fra_fwd_varlen_gather(a, None, 1 << 27, None) == _lib.FRA_OK
+    assert lib.fra_fwd_varlen_gather(a, _rope(), 1 << 27, None) == _lib.FRA_OK

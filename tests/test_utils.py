@@ -144,3 +144,26 @@ def test_full_cu_seqlens_matches_hf_form():
     want = torch.nn.functional.pad(torch.repeat_interleave(thw[:, 1] * thw[:, 2], thw[:, 0]).cumsum(0), (1, 0))
     np.testing.assert_array_equal(owin.full_cu_seqlens(grids, per_frame=True), want.numpy())
     assert owin.full_cu_seqlens(grids, per_frame=False)[-1] == int((thw[:, 0] * thw[:, 1] * thw[:, 2]).sum())
+
+
+# ---- window_row_index: window_shuffle's gather as a row index --------------------------
+
+@pytest.mark.parametrize("name", ROPE_SETS)
+def test_window_row_index_is_the_shuffle_gather(name):
+    from fused_rope_attn_amd.utils import window_row_index
+    grids = [tuple(int(x) for x in g) for g in ROPE[f"{name}/grids"]]
+    _, m, _, _ = (int(x) for x in ROPE[f"{name}/params"])
+    widx = torch.from_numpy(ROPE[f"{name}/window_index"])
+    rows = window_row_index(widx, spatial_merge_size=m)
+    n = int(widx.numel()) * m * m
+    assert rows.dtype == torch.int32 and rows.shape == (n,)
+    assert torch.equal(torch.sort(rows.long()).values, torch.arange(n))  # a permutation
+    x = torch.randn(n, 3)
+    assert torch.equal(x[rows.long()], window_shuffle(x, widx, spatial_merge_size=m))
+    assert torch.equal(window_unshuffle(x[rows.long()], widx, spatial_merge_size=m), x)
+
+
+def test_window_row_index_value_error():
+    from fused_rope_attn_amd.utils import window_row_index
+    with pytest.raises(ValueError, match=r"^spatial_merge_size must be > 0, got 0$"):
+        window_row_index(torch.arange(4), spatial_merge_size=0)
