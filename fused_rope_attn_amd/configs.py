@@ -12,6 +12,8 @@ them into ``cu_seqlens`` and cos/sin tables with this package's own
 * ``cfg3``  six images with grids 34x46, 22x66, 50x50, 16x80, 72x38 (merge 2)
   and 31x31 (merge 1: an odd grid cannot be merged 2x2), window layer with
   partial edge windows, H=16, D=80
+* ``cfg3f`` the same six images as full-attention segments (one per image:
+  1564, 1452, 2500, 1280, 2736 and 961 tokens), H=16, D=80
 * ``cfg4v`` Qwen3-VL-style video, 8 temporal groups of a 48x48 grid, one
   segment per group (8 x 2304), H=16, D=72
 * ``cfg4s`` the same tokens as a single 18432-token segment
@@ -50,6 +52,9 @@ WORKLOADS = {
     "cfg2f": Workload("cfg2f", ((((1, 96, 96),), 2),), "full", note="1344^2 full-attention layer"),
     "cfg3": Workload("cfg3", ((((1, 34, 46), (1, 22, 66), (1, 50, 50), (1, 16, 80), (1, 72, 38)), 2),
                               (((1, 31, 31),), 1)), "window", note="ragged 6-image window layer"),
+    "cfg3f": Workload("cfg3f", ((((1, 34, 46), (1, 22, 66), (1, 50, 50), (1, 16, 80), (1, 72, 38)), 2),
+                                (((1, 31, 31),), 1)), "full",
+                      note="ragged 6-image full-attention layer"),
     "cfg4v": Workload("cfg4v", ((((8, 48, 48),), 2),), "full", head_dim=72, patch_size=16,
                       note="video, 8 x 2304-token segments"),
     "cfg4s": Workload("cfg4s", ((((8, 48, 48),), 2),), "full_single", head_dim=72, patch_size=16,

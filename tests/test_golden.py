@@ -106,7 +106,7 @@ def _hf_tables(grids, d, m, widx):
     return emb.cos().numpy(), emb.sin().numpy()
 
 
-@pytest.mark.parametrize("wl", ["cfg0", "cfg1", "cfg2w", "cfg3", "cfg4v"])
+@pytest.mark.parametrize("wl", ["cfg0", "cfg1", "cfg2w", "cfg3", "cfg3f", "cfg4v"])
 def test_workload_layouts_match_transformers(wl):
     from fused_rope_attn_amd.configs import WORKLOADS, layout
     w = WORKLOADS[wl]

@@ -290,7 +290,7 @@ def test_graph_capture_replays(device):
 
 WORKLOAD_HEADS = {  # heads checked against the oracle at full size
     "cfg0": None, "cfg1": None, "cfg2w": None, "cfg3": None,
-    "cfg2f": [0, 15], "cfg4v": [0, 9], "cfg4s": [5],
+    "cfg2f": [0, 15], "cfg3f": [0, 11], "cfg4v": [0, 9], "cfg4s": [5],
 }
 
 
