@@ -328,7 +328,8 @@ __device__ __forceinline__ void bwd_dq_unit(const BParams &p, char *lds, int uni
     constexpr int kKr = LDS::kKr, kV = LDS::kV;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 31, g = lane >> 5;
-    const int sh = unit / p.blocks, qb = unit - sh * p.blocks;
+    const int pi = unit / p.blocks, qb = unit - pi * p.blocks;
+    const int sh = long_pair(pi, p.num_seqs * p.num_heads);
     const int seg = sh / p.num_heads, head = sh - seg * p.num_heads;
     int s0, L;
     seg_bounds(p, seg, s0, L);
@@ -478,7 +479,8 @@ __device__ __forceinline__ void bwd_dkdv_unit(const BParams &p, char *lds, int u
     constexpr int kQr = LDS::kQr, kDo = LDS::kDo, kLse = LDS::kLse, kDv = LDS::kDv;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 31, g = lane >> 5;
-    const int sh = unit / p.blocks, kb = unit - sh * p.blocks;
+    const int pi = unit / p.blocks, kb = unit - pi * p.blocks;
+    const int sh = long_pair(pi, p.num_seqs * p.num_heads);
     const int seg = sh / p.num_heads, head = sh - seg * p.num_heads;
     int s0, L;
     seg_bounds(p, seg, s0, L);

@@ -97,6 +97,32 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
     return xcd < rem ? xcd * (base + 1) + local : rem * (base + 1) + (xcd - rem) * base + local;
 }
 
+// ---- unit order of the long kernels (forward and backward) ----------------------------
+//
+// Units u = (pair position i, block) with u = i * blocks + block, and
+// pairs (segment, head) sh = seg * heads + head taken in an order that deals
+// them out to the eight XCDs by residue: position i is pair 8k + r for the
+// i-th (r, k) in r-major order.  xcd_remap gives XCD x a contiguous range of
+// units, so XCD x works on pairs x, x + 8, x + 16, ...: the heads of every
+// segment are spread over all XCDs, which keeps layers of unequal segments
+// balanced (in segment order, one XCD took nearly all units of the longest
+// image of a ragged batch), while the query blocks of one pair stay on one
+// XCD, sharing its K/V rows in L2.
+__device__ __forceinline__ int long_pair(int i, int pairs) {
+    const int q = pairs >> 3, rem = pairs & 7;
+    const int big = rem * (q + 1);  // the first rem residues hold q + 1 pairs
+    int r, k;
+    if (i < big) {
+        r = i / (q + 1);
+        k = i - r * (q + 1);
+    } else {
+        const int j = i - big;
+        r = rem + j / q;
+        k = j - (j / q) * q;
+    }
+    return 8 * k + r;
+}
+
 // v_permlane32_swap with both operands in a and b: lanes 32..63 of a trade
 // places with lanes 0..31 of b, so when both start as x, one of them holds
 // x of lanes 0..31 in both halves and the other x of lanes 32..63.  It is a

@@ -756,32 +756,6 @@ __global__ __launch_bounds__(256) void krot_kernel(const KParams p) {
     *(u32x2 *)(dst + 2 * HALF + 8 * i) = r1;
 }
 
-// ---- unit order of the long kernel ---------------------------------------------------
-//
-// Units u = (pair position i, query block) with u = i * qblocks + qblk, and
-// pairs (segment, head) sh = seg * heads + head taken in an order that deals
-// them out to the eight XCDs by residue: position i is pair 8k + r for the
-// i-th (r, k) in r-major order.  xcd_remap gives XCD x a contiguous range of
-// units, so XCD x works on pairs x, x + 8, x + 16, ...: the heads of every
-// segment are spread over all XCDs, which keeps layers of unequal segments
-// balanced (in segment order, one XCD took nearly all units of the longest
-// image of a ragged batch), while the query blocks of one pair stay on one
-// XCD, sharing its K/V rows in L2.
-__device__ __forceinline__ int long_pair(int i, int pairs) {
-    const int q = pairs >> 3, rem = pairs & 7;
-    const int big = rem * (q + 1);  // the first rem residues hold q + 1 pairs
-    int r, k;
-    if (i < big) {
-        r = i / (q + 1);
-        k = i - r * (q + 1);
-    } else {
-        const int j = i - big;
-        r = rem + j / q;
-        k = j - (j / q) * q;
-    }
-    return 8 * k + r;
-}
-
 // ---- split last round: partial results and their merge ------------------------
 //
 // Workspace: per (split unit, part), kLongBQ rows of split_row_floats(D) floats:
