@@ -15,6 +15,11 @@ Translation units, compiled in parallel:
 ``FRA_BUILD_DIMS=80,72`` (environment) builds only those head dims, for
 quicker iteration on a kernel; the library then reports every other head_dim
 as unsupported.  The default builds all.
+
+The kernel units are compiled with the compiler's resource-usage remarks,
+and the build fails if a kernel uses scratch memory (register spills) that
+``SCRATCH_ALLOWED`` does not list: the instances the benchmark workloads run
+must stay spill-free, and every known spill is listed with its size.
 """
 import os
 import re
@@ -29,6 +34,47 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libfra.so")
 ARCH = "gfx950"
+
+
+# (mangled-name pattern, largest scratch bytes per lane allowed): instances
+# that spill, all off the BASELINE workloads' paths -- head_dim 128 long
+# kernels (fp32 full-width tables without the rotated-K workspace: up to 496
+# B; with it 316 B; 16-bit or half-width tables: 8-20 B), head_dim 96 long
+# kernels with fp32 full-width tables rotating K in the kernel (100-112 B),
+# fp16 window kernels at head_dim 80 with two heads per workgroup (20-36 B),
+# head_dim 96 window kernels with full-width tables (20-36 B) and the
+# head_dim 96 backward long kernel (16 B).
+SCRATCH_ALLOWED = [
+    (r"long_kernelILi128E", 512),
+    (r"long_kernelILi96E.*Li2ELb1ELb0E", 128),
+    (r"window_kernelILi80ENS_3F16E", 64),
+    (r"window_kernelILi96E.*ELb1ELi2E", 64),
+    (r"bwd_long_kernelILi96E", 32),
+]
+
+
+def scratch_use(remarks: str) -> dict:
+    """{kernel symbol: scratch bytes per lane} from -Rpass-analysis=kernel-resource-usage output."""
+    out, cur = {}, None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            cur = m.group(1)
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and cur:
+            out[cur] = int(m.group(1))
+    return out
+
+
+def check_scratch(use: dict) -> list:
+    """Kernels whose scratch use SCRATCH_ALLOWED does not cover."""
+    bad = []
+    for name, nbytes in sorted(use.items()):
+        if nbytes == 0:
+            continue
+        if not any(re.search(pat, name) and nbytes <= cap for pat, cap in SCRATCH_ALLOWED):
+            bad.append(f"{name}: {nbytes} B/lane of scratch")
+    return bad
 
 
 def hipcc() -> str:
@@ -85,11 +131,12 @@ def units(tmpd: str) -> list:
     if os.environ.get("FRA_BUILD_DIMS", "").strip():
         common = ["-DFRA_HEAD_DIMS(X)=" + " ".join(f"X({d})" for d in dims)]
     out = [(os.path.join(CSRC, s), os.path.join(tmpd, s + ".o"), common) for s in ("fra_fwd.hip", "fra_bwd.hip")]
+    usage = ["-Rpass-analysis=kernel-resource-usage"]
     for d in dims:
         out.append((os.path.join(CSRC, "fra_inst_fwd.hip"), os.path.join(tmpd, f"fra_inst_fwd_d{d}.o"),
-                    common + [f"-DFRA_HEAD_DIM={d}"]))
+                    common + [f"-DFRA_HEAD_DIM={d}"] + usage))
         out.append((os.path.join(CSRC, "fra_inst_bwd.hip"), os.path.join(tmpd, f"fra_inst_bwd_d{d}.o"),
-                    common + [f"-DFRA_HEAD_DIM={d}"]))
+                    common + [f"-DFRA_HEAD_DIM={d}"] + usage))
     return out
 
 
@@ -102,19 +149,26 @@ def build(verbose: bool = False) -> str:
         if verbose:
             for c, _ in todo:
                 print(" ".join(c), flush=True)
-        errs, running = [], []
+        errs, running, use = [], [], {}
         while todo or running:
             while todo and len(running) < jobs:
                 c, _ = todo.pop(0)
                 running.append((c, subprocess.Popen(c, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
             c, pr = running.pop(0)
             _, err = pr.communicate()
+            use.update(scratch_use(err))
+            err = "\n".join(l for l in err.splitlines() if "kernel-resource-usage" not in l and l.strip() != "|"
+                            and not re.match(r"^\s*\d+ \|", l) and not re.match(r"^\s*\|\s*\^", l)
+                            and not l.startswith("In file included from"))
             if pr.returncode != 0:
                 errs.append(f"hipcc failed ({pr.returncode}) on {' '.join(c[-3:])}:\n{_clean(err)}")
             elif verbose and _clean(err).strip():
                 print(_clean(err), file=sys.stderr)
         if errs:
             raise RuntimeError("\n".join(errs))
+        bad = check_scratch(use)
+        if bad:
+            raise RuntimeError("kernels spill to scratch memory outside build.SCRATCH_ALLOWED:\n" + "\n".join(bad))
         tmp = LIB + ".tmp"
         cmd = link_command(objs, tmp)
         if verbose:
