@@ -382,10 +382,15 @@ def fused_rope_attention(
                                "(q, k or v requires grad)")
         if rows is not None:
             raise RuntimeError("fused_rope_attention(): row_index is forward only (q, k or v requires grad)")
-        return _FusedRopeAttention.apply(q, k, v, cos, sin, cu, max_seqlen, scale)
+        return torch.ops.fused_rope_attn_amd.fwd(q, k, v, cos, sin, cu, max_seqlen, scale, True)[0]
+    if rows is not None:
+        if out is None:
+            out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        return _forward(q, k, v, cos, sin, cu, max_seqlen, scale, out, None, rows)
     if out is None:
-        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    return _forward(q, k, v, cos, sin, cu, max_seqlen, scale, out, None, rows)
+        return torch.ops.fused_rope_attn_amd.fwd(q, k, v, cos, sin, cu, max_seqlen, scale, False)[0]
+    torch.ops.fused_rope_attn_amd.fwd_out(q, k, v, cos, sin, cu, max_seqlen, scale, out)
+    return out
 
 
 def _prepare_rows(row_index, q):
@@ -571,30 +576,76 @@ def fused_rope_attention_bwd(dout, q, k, v, cos, sin, out, lse, cu_seqlens, max_
     return _backward(dout, q, k, v, cos, sin, out, lse, cu, int(max_seqlen), scale, dq, dk, dv)
 
 
-class _FusedRopeAttention(torch.autograd.Function):
-    """Autograd node of the op: the forward also writes the log-sum-exp, the
-    backward runs ``fra_bwd_varlen``.  cos/sin and cu_seqlens get no
-    gradient; the backward is not itself differentiable (double backward
-    raises)."""
+# ---------------------------------------------------------------------------
+# torch.library registration: the op as custom ops with fake (meta)
+# implementations and an autograd formula, so that torch.compile and
+# torch.export trace through it (the ctypes call is opaque to them).
+# ---------------------------------------------------------------------------
 
-    @staticmethod
-    def forward(ctx, q, k, v, cos, sin, cu, max_seqlen, scale):
-        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-        lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
-        _forward(q, k, v, cos, sin, cu, max_seqlen, scale, out, lse)
-        ctx.save_for_backward(q, k, v, cos, sin, out, lse, cu)
-        ctx.max_seqlen, ctx.scale = max_seqlen, scale
-        return out
+@torch.library.custom_op("fused_rope_attn_amd::fwd", mutates_args=(), device_types="cuda")
+def _fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+            cu: torch.Tensor, max_seqlen: int, scale: float, with_lse: bool) -> "tuple[torch.Tensor, torch.Tensor]":
+    """Forward into a fresh ``out`` (and ``lse`` [heads, tokens] fp32 when
+    ``with_lse``; else an empty tensor).  Inputs validated by the caller."""
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty((q.shape[1], q.shape[0]) if with_lse else (0,), dtype=torch.float32, device=q.device)
+    _forward(q, k, v, cos, sin, cu, max_seqlen, scale, out, lse if with_lse else None)
+    return out, lse
 
-    @staticmethod
-    @torch.autograd.function.once_differentiable
-    def backward(ctx, dout):
-        q, k, v, cos, sin, out, lse, cu = ctx.saved_tensors
-        dq = torch.zeros(q.shape, dtype=q.dtype, device=q.device)
-        dk = torch.zeros(q.shape, dtype=q.dtype, device=q.device)
-        dv = torch.zeros(q.shape, dtype=q.dtype, device=q.device)
-        _backward(dout, q, k, v, cos, sin, out, lse, cu, ctx.max_seqlen, ctx.scale, dq, dk, dv)
-        return dq, dk, dv, None, None, None, None, None
+
+@_fwd_op.register_fake
+def _fwd_fake(q, k, v, cos, sin, cu, max_seqlen, scale, with_lse):
+    return (q.new_empty(q.shape),
+            q.new_empty((q.shape[1], q.shape[0]) if with_lse else (0,), dtype=torch.float32))
+
+
+@torch.library.custom_op("fused_rope_attn_amd::fwd_out", mutates_args=("out",), device_types="cuda")
+def _fwd_out_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                cu: torch.Tensor, max_seqlen: int, scale: float, out: torch.Tensor) -> None:
+    """Forward into the caller's ``out`` (rows outside every segment keep
+    their contents)."""
+    _forward(q, k, v, cos, sin, cu, max_seqlen, scale, out, None)
+
+
+@_fwd_out_op.register_fake
+def _fwd_out_fake(q, k, v, cos, sin, cu, max_seqlen, scale, out):
+    return None
+
+
+@torch.library.custom_op("fused_rope_attn_amd::bwd", mutates_args=(), device_types="cuda")
+def _bwd_op(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+            sin: torch.Tensor, out: torch.Tensor, lse: torch.Tensor, cu: torch.Tensor, max_seqlen: int,
+            scale: float) -> "tuple[torch.Tensor, torch.Tensor, torch.Tensor]":
+    """Gradients of ``fwd`` (zero in rows outside every segment).  Has no
+    autograd formula itself: a double backward raises."""
+    dq = torch.zeros(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.zeros(q.shape, dtype=q.dtype, device=q.device)
+    dv = torch.zeros(q.shape, dtype=q.dtype, device=q.device)
+    _backward(dout, q, k, v, cos, sin, out, lse, cu, max_seqlen, scale, dq, dk, dv)
+    return dq, dk, dv
+
+
+@_bwd_op.register_fake
+def _bwd_fake(dout, q, k, v, cos, sin, out, lse, cu, max_seqlen, scale):
+    return q.new_empty(q.shape), q.new_empty(q.shape), q.new_empty(q.shape)
+
+
+def _fwd_setup_context(ctx, inputs, output):
+    q, k, v, cos, sin, cu, max_seqlen, scale, _with_lse = inputs
+    out, lse = output
+    ctx.save_for_backward(q, k, v, cos, sin, out, lse, cu)
+    ctx.max_seqlen, ctx.scale = max_seqlen, scale
+    ctx.mark_non_differentiable(lse)
+
+
+def _fwd_backward(ctx, dout, _dlse):
+    """cos/sin and cu_seqlens get no gradient."""
+    q, k, v, cos, sin, out, lse, cu = ctx.saved_tensors
+    dq, dk, dv = torch.ops.fused_rope_attn_amd.bwd(dout, q, k, v, cos, sin, out, lse, cu, ctx.max_seqlen, ctx.scale)
+    return dq, dk, dv, None, None, None, None, None, None
+
+
+_fwd_op.register_autograd(_fwd_backward, setup_context=_fwd_setup_context)
 
 
 # ---------------------------------------------------------------------------
