@@ -383,14 +383,17 @@ def fused_rope_attention(
         if rows is not None:
             raise RuntimeError("fused_rope_attention(): row_index is forward only (q, k or v requires grad)")
         return torch.ops.fused_rope_attn_amd.fwd(q, k, v, cos, sin, cu, max_seqlen, scale, True)[0]
-    if rows is not None:
+    if torch.compiler.is_compiling() and rows is None:
+        # traced (torch.compile / export): through the custom ops
         if out is None:
-            out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-        return _forward(q, k, v, cos, sin, cu, max_seqlen, scale, out, None, rows)
+            return torch.ops.fused_rope_attn_amd.fwd(q, k, v, cos, sin, cu, max_seqlen, scale, False)[0]
+        torch.ops.fused_rope_attn_amd.fwd_out(q, k, v, cos, sin, cu, max_seqlen, scale, out)
+        return out
+    # eager: straight to the library (the dispatcher round trip of a custom
+    # op costs host time a back-to-back stream of layers then waits on)
     if out is None:
-        return torch.ops.fused_rope_attn_amd.fwd(q, k, v, cos, sin, cu, max_seqlen, scale, False)[0]
-    torch.ops.fused_rope_attn_amd.fwd_out(q, k, v, cos, sin, cu, max_seqlen, scale, out)
-    return out
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    return _forward(q, k, v, cos, sin, cu, max_seqlen, scale, out, None, rows)
 
 
 def _prepare_rows(row_index, q):
