@@ -1335,6 +1335,11 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
                                        E::pack(cur[a][8 * h + 4], cur[a][8 * h + 5]),
                                        E::pack(cur[a][8 * h + 6], cur[a][8 * h + 7])};
         }
+        // P(j) is complete here.  Without the pin the compiler sinks the
+        // exponentials and packs to their use, past the ping-pong barrier
+        // into phase B, in front of the PV MFMAs that wait for them.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(pop[i]));
     };
     auto iteration_steady = [&](auto par_tag, int j, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
         constexpr int P = decltype(par_tag)::value;
@@ -1445,14 +1450,18 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
                 constexpr int P = decltype(par_tag)::value;
                 u32x4 pop[4];
                 issue(grp == 0, P);  // group 0: K_rot(jj+2); group 1: V(jj+1)
-                smax(cur, kLongBKV);
                 phase_a(jj, cur, nxt, pop);
                 half_barrier(grp == 0 ? nk : nv);
                 if (grp == 0) issue(false, P);      // V(jj+1)
                 else if (more) issue(true, P ^ 1);  // K_rot(jj+3)
                 pv(jj, pop);
+                // Row max of S(jj+1) (a full block) beside the PV MFMAs, whose
+                // VALU slots are otherwise empty; a rescale of O waits for
+                // them, which it must (O then holds block jj).
+                smax(nxt, kLongBKV);
                 half_barrier(grp == 0 ? nv : (more ? nk : 0));
             };
+            smax(sA, kLongBKV);  // S(0), a full block
             if (grp == 1) {  // K_rot(2), which group 0 issues with A(0)
                 issue(true, 0);
                 half_barrier(nk);
