@@ -55,12 +55,17 @@ __host__ __device__ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 __host__ __device__ constexpr int cmin(int a, int b) { return a < b ? a : b; }
 __host__ __device__ constexpr int bwd_dp(int d) { return (d + 15) / 16 * 16; }
 
-// LDS row pitch (bytes) of a region read both as rows (16-byte reads) and
-// transposed (ds_read_b64_tr_b16): 4 or 12 mod 16 chunks of 16 bytes (16 or
-// 48 mod 64 dwords) keeps the transposed reads conflict-free.
+// LDS row pitch (bytes) of a region read both as rows (16-byte MFMA operand
+// reads) and transposed (ds_read_b64_tr_b16 over 32-column tiles, so up to
+// 4 * ceil(d / 32) chunks of 16 bytes per row): an odd chunk count.  Rows
+// read as 16-byte operands are then conflict-free and the transposed reads
+// at most 2-way; a pitch of 4 or 12 mod 16 chunks makes the transposed reads
+// conflict-free but puts rows r and r + 4 on the same banks, a 4-way
+// conflict on every row read (measured 2.7e8 conflict cycles per backward
+// call at 9216 tokens x 16 heads, about a quarter of the kernel's time).
 __host__ __device__ constexpr int bwd_pitch_tr(int d) {
-    int c = bwd_dp(d) / 8;
-    while (c % 16 != 4 && c % 16 != 12) ++c;
+    int c = cmax(bwd_dp(d) / 8, 4 * ((d + 31) / 32));
+    if (c % 2 == 0) ++c;
     return 16 * c;
 }
 // ... and of a region read only as rows: an odd chunk count.
@@ -941,10 +946,11 @@ namespace fra_internal {
 
 template <int D, class E, bool FULL, int NW>
 BwdKernels bwd_kernels_nw() {
-    // No register-V instance at D = 96 with full-width tables (it spills),
-    // nor at D >= 128, where it would fit no more workgroups per CU than the
-    // staged kernel (two) and so could never be chosen.
-    constexpr bool kVreg = !(D == 96 && FULL) && D < 128;
+    // A register-V instance only where it fits more workgroups per CU than
+    // the staged kernel (the planner could never choose it otherwise: D = 64,
+    // whose staged kernel fits four, and D >= 128, two either way), and not
+    // at D = 96 with full-width tables (it spills).
+    constexpr bool kVreg = !(D == 96 && FULL) && WinBwdLds<D, true>::kPerCu > WinBwdLds<D, false>::kPerCu;
     BwdFn vreg = nullptr;
     if constexpr (kVreg) vreg = (BwdFn)bwd_window_kernel<D, E, FULL, true>;
     return BwdKernels{(BwdFn)bwd_dot_kernel<D, E>,

@@ -102,7 +102,9 @@ CASES = [
     # with V in registers, four workgroups per CU
     ([64] * 52 + [17, 0, 5, 33], 16, 80, None, torch.bfloat16, 0, 0, "bwd_window_vreg"),
     ([64] * 58 + [40, 2], 16, 72, 72, torch.float16, 0, 2, "bwd_window_vreg"),
-    ([64] * 49 + [1], 16, 64, None, torch.bfloat16, 3, 0, "bwd_window_vreg"),
+    # head_dim 64: the staged kernel fits four workgroups per CU itself, so
+    # the same grid runs it (no register-V instance is built there)
+    ([64] * 49 + [1], 16, 64, None, torch.bfloat16, 3, 0, "bwd_window_d64"),
     # head_dim 96 window backward: half-width tables with the register-V
     # instance (grid in (3, 4] x CUs) and the staged one (below it); full
     # width (no register-V instance); head_dim 128 (the forward sends it to
