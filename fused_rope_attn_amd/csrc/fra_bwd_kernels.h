@@ -80,6 +80,10 @@ template <int D> struct BwdOcc {
     static constexpr int kWaves = D >= 128 ? 1 : 2;
 };
 
+// sched_barrier mask: VALU, SALU and transcendental instructions may be
+// scheduled across it; LDS accesses and MFMAs keep their written order.
+constexpr int kSchedValuMayCross = 0x0002 | 0x0004 | 0x0400;
+
 constexpr int kBwdBlockQ = 64;   // queries per LDS stage of the dk/dv kernel
 constexpr int kBwdBlockKV = 64;  // keys per LDS stage of the dq kernel
 
@@ -405,17 +409,29 @@ __device__ __forceinline__ void bwd_dq_unit(const BParams &p, char *lds, int uni
         }
         const char *const stage = lds + (kb & 1) * LDS::kStage;
         // S^T = K_rot Q_rot^T and dP^T = V dout^T: rows key, column query.
+        // Tile a = 0's two chains, then tile 1's, alternating S and dP; each
+        // MFMA's LDS operand is read two MFMAs ahead (read just before its
+        // MFMA, every operand's latency was exposed), and the VALU work of
+        // tile 0's dZ may move in beside tile 1's MFMAs.
         f32x16 sacc[2], dpacc[2];
+        {
+            constexpr int NM = 4 * S;
+            auto oaddr = [&](int i) {
+                const int a = i / (2 * S), t = (i % (2 * S)) >> 1;
+                return (i & 1) ? stage + kV + (32 * a + r) * PRD + 32 * t + 16 * g
+                               : stage + kKr + (32 * a + r) * PTR + 32 * t + 16 * g;
+            };
+            u32x4 op[3];
+            op[0] = *(const u32x4 *)oaddr(0);
+            op[1] = *(const u32x4 *)oaddr(1);
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
-            sacc[a] = f32x16{};
-            dpacc[a] = f32x16{};
-#pragma unroll
-            for (int t = 0; t < S; ++t)
-                sacc[a] = E::mma(*(const u32x4 *)(stage + kKr + (32 * a + r) * PTR + 32 * t + 16 * g), qop[t], sacc[a]);
-#pragma unroll
-            for (int t = 0; t < S; ++t)
-                dpacc[a] = E::mma(*(const u32x4 *)(stage + kV + (32 * a + r) * PRD + 32 * t + 16 * g), dop[t], dpacc[a]);
+            for (int i = 0; i < NM; ++i) {
+                if (i + 2 < NM) op[(i + 2) % 3] = *(const u32x4 *)oaddr(i + 2);
+                const int a = i / (2 * S), t = (i % (2 * S)) >> 1;
+                if (i & 1) dpacc[a] = E::mma(op[i % 3], dop[t], t == 0 ? f32x16{} : dpacc[a]);
+                else sacc[a] = E::mma(op[i % 3], qop[t], t == 0 ? f32x16{} : sacc[a]);
+                __builtin_amdgcn_sched_barrier(kSchedValuMayCross);
+            }
         }
         // dZ^T = P^T * (dP^T - Dvec), keys past the segment masked.
         u32x4 dsop[2][2];
@@ -573,13 +589,26 @@ __device__ __forceinline__ void bwd_dkdv_unit(const BParams &p, char *lds, int u
         for (int a = 0; a < 2; ++a) {
             if (32 * a >= nq) break;  // uniform
             // S = Q_rot K_rot^T and dP = dout V^T: rows query, column key.
-            f32x16 sacc = f32x16{}, dpacc = f32x16{};
+            // The two chains alternate; each MFMA's LDS operand is read two
+            // MFMAs ahead.
+            f32x16 sacc, dpacc;
+            {
+                constexpr int NM = 2 * S;
+                auto oaddr = [&](int i) {
+                    return stage + ((i & 1) ? kDo : kQr) + (32 * a + r) * PTR + 32 * (i >> 1) + 16 * g;
+                };
+                u32x4 op[3];
+                op[0] = *(const u32x4 *)oaddr(0);
+                op[1] = *(const u32x4 *)oaddr(1);
 #pragma unroll
-            for (int t = 0; t < S; ++t)
-                sacc = E::mma(*(const u32x4 *)(stage + kQr + (32 * a + r) * PTR + 32 * t + 16 * g), kop[t], sacc);
-#pragma unroll
-            for (int t = 0; t < S; ++t)
-                dpacc = E::mma(*(const u32x4 *)(stage + kDo + (32 * a + r) * PTR + 32 * t + 16 * g), vop[t], dpacc);
+                for (int i = 0; i < NM; ++i) {
+                    if (i + 2 < NM) op[(i + 2) % 3] = *(const u32x4 *)oaddr(i + 2);
+                    const int t = i >> 1;
+                    if (i & 1) dpacc = E::mma(op[i % 3], vop[t], t == 0 ? f32x16{} : dpacc);
+                    else sacc = E::mma(op[i % 3], kop[t], t == 0 ? f32x16{} : sacc);
+                    __builtin_amdgcn_sched_barrier(kSchedValuMayCross);
+                }
+            }
             // Element j holds query 32a + 8(j/4) + 4g + (j%4).
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
