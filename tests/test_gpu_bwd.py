@@ -98,6 +98,9 @@ CASES = [
     ([200], 1, 96, 96, torch.bfloat16, 0, 0),                 # long, full-width tables
     ([150, 70], 2, 128, None, torch.float16, 0, 0),           # long, head_dim 128, fp16
     ([1000], 1, 80, None, torch.bfloat16, 0, 0),              # long, many key/query blocks
+    # long, 10 (segment, head) pairs: more than eight, not a multiple of
+    # eight, so the units' deal to the XCDs takes its general branch
+    ([300, 1, 64, 0, 200], 2, 80, None, torch.bfloat16, 0, 2),
     # window grids of 768 < segments x heads <= 1024 (256 CUs): the variant
     # with V in registers, four workgroups per CU
     ([64] * 52 + [17, 0, 5, 33], 16, 80, None, torch.bfloat16, 0, 0, "bwd_window_vreg"),
