@@ -6,6 +6,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -219,20 +220,35 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true,
     kp.ws = nullptr;
     kp.dense_heads = a->q_stride_head == d && a->k_stride_head == d && a->v_stride_head == d && a->out_stride_head == d;
     if (window) {
-        // Two heads per workgroup when that grid still runs in one round of
+        // Heads per workgroup.  Two when that grid still runs in one round of
         // resident workgroups (shorter per-workgroup chains: measured 2.6%
         // faster at 144 windows x 16 heads, 4% at 16 windows), else four.
-        {
+        // One head, its two query tiles on two wavefronts, when there are
+        // no more (segment, head) pairs than CUs, where two-head workgroups
+        // would leave CUs idle (16 windows x 16 heads: 13.5 against 14.5 us;
+        // at 64 windows, four pairs a CU, the duplicated K staging made it
+        // 6% slower than two heads).  FRA_WINDOW_HEADS=1, 2 or 4 forces a
+        // form that has an instance (tests and tuning).
+        int want = 0;
+        if (const char *e = getenv("FRA_WINDOW_HEADS")) want = atoi(e);
+        if (want != 1 && want != 2 && want != 4) want = 0;
+        if (want != 4) {
             const int64_t g2 = (int64_t)a->num_seqs * ((a->num_heads + 1) / 2);
             Choice c2;
             memset(&c2, 0, sizeof(c2));
             pick_kernel(d, true, 2, full, a->qkv_dtype, rd, c2);
-            if (g2 <= (int64_t)device_cus() * c2.per_cu) c = c2;
+            if (c2.fn && (want == 2 || (want == 0 && g2 <= (int64_t)device_cus() * c2.per_cu))) c = c2;
+        }
+        if (want == 0 || want == 1) {
+            Choice c1;
+            memset(&c1, 0, sizeof(c1));
+            pick_kernel(d, true, 1, full, a->qkv_dtype, rd, c1);
+            if (c1.fn && (want == 1 || sh <= (int64_t)device_cus())) c = c1;
         }
         kp.qblocks = 1;
         grid = (int64_t)a->num_seqs * ((a->num_heads + c.heads - 1) / c.heads);
         c.kernel = FRA_KERNEL_WINDOW;
-        c.block = 64 * c.heads;
+        c.block = 64 * (c.heads == 1 ? 2 : c.heads);
         c.block_q = 64;
         c.block_kv = 64;
         snprintf(c.name, sizeof(c.name), "window_d%d_%s_rope%s%s", d, dtype_name(a->qkv_dtype), dtype_name(rd),

@@ -202,14 +202,23 @@ template <int D, bool FULL, int HW> struct WinLds {
     // spills), else two.
     static constexpr int kWaves = !FULL && D <= 80 && D % 16 == 0 && 3 * kBytes <= 160 * 1024 ? 3 : 2;
     // Workgroups per CU (LDS and wavefronts per SIMD), for the planner.
-    static constexpr int kPerCu = (160 * 1024 / kBytes) < (4 * kWaves / HW) ? (160 * 1024 / kBytes) : (4 * kWaves / HW);
+    // Wavefronts per workgroup: one per head, except HW = 1, where two
+    // wavefronts split the head's 64 queries (one 32-query tile each).
+    static constexpr int kWgWaves = HW == 1 ? 2 : HW;
+    static constexpr int kPerCu = (160 * 1024 / kBytes) < (4 * kWaves / kWgWaves) ? (160 * 1024 / kBytes) : (4 * kWaves / kWgWaves);
 };
 
 template <int D, class E, int RD, bool FULL, int HW, bool GATHER>
-__global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window_kernel(const KParams p) {
+__global__ __launch_bounds__((64 * WinLds<D, FULL, HW>::kWgWaves), (WinLds<D, FULL, HW>::kWaves)) void window_kernel(const KParams p) {
     using LDS = WinLds<D, FULL, HW>;
     constexpr int kWinHeads = HW;
-    constexpr int kWinThreads = 64 * HW;
+    constexpr int kWinWaves = LDS::kWgWaves;
+    constexpr int kWinThreads = 64 * kWinWaves;
+    // HW = 1 (query split): both wavefronts work on the one head; wavefront
+    // w rotates the queries of tile w and attends them (a layer with few
+    // (segment, head) pairs gets twice the wavefronts, each with half the
+    // chain).  Otherwise wavefront w owns head w of the group, both tiles.
+    constexpr bool QSPLIT = HW == 1;
     constexpr int NQ = D / 8;                 // quads per half
     constexpr int S = (NQ + 1) / 2;           // 16-deep k-steps of QK^T
     constexpr int NDT = LDS::NDT;
@@ -229,7 +238,7 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
     // Item k of a slab belongs to half k / (SPER / 2) when a half is a whole
     // number of item rounds (D != 72); otherwise it is tested per item.
     constexpr bool KHALF = 32 * NCH % kWinThreads == 0;
-    constexpr int VPER = (VPC + kWinHeads - 1) / kWinHeads;  // V direct loads per wavefront
+    constexpr int VPER = (VPC + kWinWaves - 1) / kWinWaves;  // V direct loads per wavefront
     typedef short v4i16 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
     typedef __attribute__((address_space(3))) void lds_void;
@@ -248,7 +257,8 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
     const int seg = u / ngroups, hg = u - seg * ngroups;
     const int h0 = hg * kWinHeads;
     const int nh = min(kWinHeads, p.num_heads - h0);            // heads in this group
-    const bool active = w < nh;  // wavefronts past the last head still take part in barriers
+    const bool active = QSPLIT || w < nh;  // wavefronts past the last head still take part in barriers
+    const int hw = QSPLIT ? 0 : w;         // this wavefront's head in the group
     int s0 = p.cu[seg], s1 = p.cu[seg + 1];
     s0 = min(max(s0, 0), p.total);
     s1 = min(max(s1, 0), p.total);
@@ -409,7 +419,7 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
     // Quad i = g*S + t exists unless NQ is odd and it is the last one.
     auto rotate_half = [&](u32x4 (&op)[S]) {
         const float *crow = tab + r * CS;
-        const char *xrow = half + r * PITCH + w * (2 * D);
+        const char *xrow = half + r * PITCH + hw * (2 * D);
 #pragma unroll
         for (int t = 0; t < S; ++t) {
             const bool maybe_pad = t >= NQ - S;   // compile time; true only for odd NQ
@@ -443,7 +453,7 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
         stage_tab(hf);
         stage_half(qs, hf);
         __syncthreads();
-        rotate_half(qop[hf]);
+        if (!QSPLIT || w == hf) rotate_half(qop[hf]);
         __syncthreads();
         stage_half(ks, hf);
         __syncthreads();
@@ -459,12 +469,12 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
         const uint32_t vrs = (uint32_t)p.sv_s * 2, vhs = (uint32_t)p.sv_h * 2;
         auto load_v = [&](auto fast_tag) {
             constexpr bool F = decltype(fast_tag)::value;
-            GridWalk<VPC, kWinThreads> it(fresh(tid));  // slot 64 (w + HW k) + lane
+            GridWalk<VPC, kWinThreads> it(fresh(tid));  // slot 64 (w + waves k) + lane
             uint32_t vro = (uint32_t)it.row * vrs;
 #pragma unroll
             for (int k = 0; k < VPER; ++k) {
-                const int m = w + kWinHeads * k;
-                if (VPC % kWinHeads == 0 || m < VPC) {  // uniform
+                const int m = w + kWinWaves * k;
+                if (VPC % kWinWaves == 0 || m < VPC) {  // uniform
                     if (it.col < NCH) {
                         const char *src;
                         if constexpr (F) src = vb + (vro + 16 * it.col);
@@ -500,7 +510,7 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
     const float sl = p.scale_log2;
     const int nkt = (L + 31) >> 5;
     const uint32_t v_lane =
-        (uint32_t)((4 * g + ((lane >> 2) & 3)) * VP + 2 * (w * D + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
+        (uint32_t)((4 * g + ((lane >> 2) & 3)) * VP + 2 * (hw * D + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)));
     // Output quad i of a tile: d0 = 32 (i / 4) + 8 (i % 4) + 4g.  Quads past
     // OQV (d0 >= D for both g) are not kept; quad OQV - 1 may be half valid.
     auto tile = [&](const u32x4 (&qcur)[S], u32x2 (&outq)[OQV], int b) {
@@ -549,7 +559,7 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
         lsum = sum_pair32(lsum);
         const float inv = 1.0f / lsum;
         if (p.lse != nullptr && g == 0 && 32 * b + r < L)
-            p.lse[(int64_t)(h0 + w) * p.total + s0 + (GATHER ? grow_bytes(32 * b + r, 1) : 32 * b + r)] =
+            p.lse[(int64_t)(h0 + hw) * p.total + s0 + (GATHER ? grow_bytes(32 * b + r, 1) : 32 * b + r)] =
                 (__builtin_amdgcn_logf(lsum) - mneg) * kLn2;
 
         // P^T as the B operand of O^T = V^T P^T: step (a, h) uses elements
@@ -590,7 +600,10 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
         }
     };
     u32x2 out0[OQV], out1[OQV];
-    if (active) {  // uniform within the wavefront; no barrier inside
+    if constexpr (QSPLIT) {
+        if (w == 0) tile(qop[0], out0, 0);
+        else if (L > 32) tile(qop[1], out0, 1);
+    } else if (active) {  // uniform within the wavefront; no barrier inside
         tile(qop[0], out0, 0);
         __builtin_amdgcn_sched_barrier(0);
         if (L > 32) tile(qop[1], out1, 1);
@@ -600,15 +613,19 @@ __global__ __launch_bounds__(64 * HW, (WinLds<D, FULL, HW>::kWaves)) void window
     // ---- 5. output rows through LDS, stored as coalesced slab rows --------------------
     if (active) {
         auto put = [&](const u32x2 (&outq)[OQV], int b) {
-            char *orow = oslab + (32 * b + r) * PITCH + w * (2 * D);
+            char *orow = oslab + (32 * b + r) * PITCH + hw * (2 * D);
 #pragma unroll
             for (int i = 0; i < OQV; ++i) {
                 const int d0 = 32 * (i / 4) + 8 * (i % 4) + 4 * g;
                 if (d0 < D) *(u32x2 *)(orow + 2 * d0) = outq[i];
             }
         };
-        put(out0, 0);
-        if (L > 32) put(out1, 1);
+        if constexpr (QSPLIT) {
+            if (w == 0 || L > 32) put(out0, w);
+        } else {
+            put(out0, 0);
+            if (L > 32) put(out1, 1);
+        }
     }
     __syncthreads();
     {
@@ -1531,7 +1548,16 @@ template <int D, class E, int RD, bool FULL> void pick_full(bool window, int hw,
     c.fn = nullptr;
     if constexpr (D <= kWindowMaxD) {
         if (window) {
-            if (hw == 2) {
+            if (hw == 1) {
+                // query split: the slab's 16-byte items must divide evenly over
+                // two wavefronts (D = 72 has nine chunks a row: no instance)
+                if constexpr (64 * (D / 8) % 128 == 0) {
+                    c.fn = (KernelFn)window_kernel<D, E, RD, FULL, 1, false>;
+                    c.fn_gather = (KernelFn)window_kernel<D, E, RD, FULL, 1, true>;
+                    c.lds = WinLds<D, FULL, 1>::kBytes;
+                    c.per_cu = WinLds<D, FULL, 1>::kPerCu;
+                }
+            } else if (hw == 2) {
                 c.fn = (KernelFn)window_kernel<D, E, RD, FULL, 2, false>;
                 c.fn_gather = (KernelFn)window_kernel<D, E, RD, FULL, 2, true>;
                 c.lds = WinLds<D, FULL, 2>::kBytes;

@@ -63,16 +63,29 @@ def plan_of(a):
     return rc, p
 
 
-def test_plan_window_and_long():
+def test_plan_window_and_long(monkeypatch):
+    monkeypatch.delenv("FRA_WINDOW_HEADS", raising=False)
     rc, p = plan_of(make_args())
     assert rc == _lib.FRA_OK
-    # one workgroup of hw wavefronts per (window, group of hw heads): hw = 2
-    # when that grid runs in one round of resident workgroups (5 per CU, 256
-    # CUs assumed without a GPU), else 4
+    # One workgroup per (window, group of hw heads).  hw = 1 (two wavefronts
+    # splitting the head's queries) when there are no more (window, head)
+    # pairs than CUs (256 assumed without a GPU); else hw = 2 when that grid
+    # runs in one round of resident workgroups (5 per CU), else 4.
     assert p.kernel == _lib.FRA_KERNEL_WINDOW and p.block == 128
-    assert p.grid == 16 * (16 // 2)
-    rc, p = plan_of(make_args(h=6))  # a partial head group
-    assert rc == _lib.FRA_OK and p.grid == 16 * 3
+    assert p.grid == 16 * 16
+    rc, p = plan_of(make_args(n=2048, nseg=32))  # 512 pairs: two heads a workgroup
+    assert rc == _lib.FRA_OK and p.block == 128 and p.grid == 32 * 8
+    rc, p = plan_of(make_args(n=4096, nseg=64, h=6))  # 384 pairs, a partial head group
+    assert rc == _lib.FRA_OK and p.grid == 64 * 3
+    # FRA_WINDOW_HEADS forces a form
+    for heads, block, grid in (("1", 128, 256), ("2", 128, 128), ("4", 256, 64)):
+        monkeypatch.setenv("FRA_WINDOW_HEADS", heads)
+        rc, p = plan_of(make_args())
+        assert rc == _lib.FRA_OK and (p.block, p.grid) == (block, grid), heads
+    monkeypatch.setenv("FRA_WINDOW_HEADS", "1")  # head_dim 72 has no one-head form: four
+    rc, p = plan_of(make_args(d=72))
+    assert rc == _lib.FRA_OK and (p.block, p.grid) == (256, 64)
+    monkeypatch.delenv("FRA_WINDOW_HEADS")
     rc, p = plan_of(make_args(n=9216, nseg=144))  # 1152 two-head workgroups fit 1280 slots
     assert rc == _lib.FRA_OK and p.block == 128 and p.grid == 144 * 8
     rc, p = plan_of(make_args(n=11968, nseg=187))  # 1496 do not: four heads

@@ -48,7 +48,12 @@ def _shuffled_route(widx, cu, q, k, v, cos, sin):
     (80, torch.bfloat16, torch.float32, True),
     (80, torch.float16, torch.float16, False),
 ])
-def test_gather_equals_shuffle_route(device, d, dtype, rope_dtype, full):
+@pytest.mark.parametrize("heads", [None, 2, 4])
+def test_gather_equals_shuffle_route(device, d, dtype, rope_dtype, full, heads, monkeypatch):
+    # heads: the window kernel's form forced through FRA_WINDOW_HEADS for
+    # both routes (None: the planner's choice)
+    if heads is not None:
+        monkeypatch.setenv("FRA_WINDOW_HEADS", str(heads))
     grids = [(1, 34, 46), (1, 16, 80), (1, 22, 66)]  # ragged edge windows
     widx, cu, rows, q, k, v, cos, sin = _image_case(grids, 6, d, d, device, dtype, rope_dtype, full)
     print(f"gather d={d} {dtype} tables {rope_dtype} full={full} tokens={q.shape[0]}", flush=True)

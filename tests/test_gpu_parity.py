@@ -81,16 +81,29 @@ WINDOW_LENS = [
 ]
 
 
+@pytest.mark.parametrize("heads", [None, 1, 2, 4])
 @pytest.mark.parametrize("d", [64, 72, 80, 96])
 @pytest.mark.parametrize("li", range(len(WINDOW_LENS)))
-def test_window_kernel_ragged(device, d, li):
+def test_window_kernel_ragged(device, d, li, heads, monkeypatch):
+    # heads: the window kernel's form forced through FRA_WINDOW_HEADS (None:
+    # the planner's choice, which for these few (segment, head) pairs is one
+    # head per workgroup with its query tiles split over two wavefronts;
+    # head_dim 72 has no such instance: the planner then takes two heads, a
+    # forced one-head form four).  Three heads leave a partial last group in
+    # the two-head form and a partial one in the four.
+    if heads is not None:
+        monkeypatch.setenv("FRA_WINDOW_HEADS", str(heads))
     lens = WINDOW_LENS[li]
     case = random_case(lens, h=3, d=d, seed=100 + li, extra_rows=5)
-    assert plan(*(case[x].to(device) for x in ("q", "k", "v", "cos", "sin", "cu_seqlens")),
-                max_seqlen=case["max_seqlen"])["kernel"] == "window" or d > 96
+    pl = plan(*(case[x].to(device) for x in ("q", "k", "v", "cos", "sin", "cu_seqlens")), max_seqlen=case["max_seqlen"])
+    assert pl["kernel"] == "window"
+    form = heads if heads is not None else 1
+    if form == 1 and d == 72:
+        form = 4 if heads == 1 else 2
+    assert pl["grid"] == len(lens) * -(-3 // form), (pl, form)
     out = f32(run_gpu(case, device))
-    assert_close(out, oracle(case), MAX_ABS, MEAN_ABS, f"window d={d} lens={lens}")
-    assert_close(out, oracle(case, "bf16"), EMU_MAX_ABS, EMU_MEAN_ABS, f"window d={d} lens={lens} (emulated)")
+    assert_close(out, oracle(case), MAX_ABS, MEAN_ABS, f"window d={d} lens={lens} heads={heads}")
+    assert_close(out, oracle(case, "bf16"), EMU_MAX_ABS, EMU_MEAN_ABS, f"window d={d} lens={lens} heads={heads} (emulated)")
 
 
 # --- long kernel --------------------------------------------------------------

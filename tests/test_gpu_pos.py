@@ -62,8 +62,13 @@ def _check(lens, h, d, seed, device, dtype=torch.bfloat16, want="window"):
     assert e.max() <= MAX_ABS and e.mean() <= MEAN_ABS, (lens, d, e.max(), e.mean())
 
 
+@pytest.mark.parametrize("heads", [None, 2, 4])
 @pytest.mark.parametrize("d", [64, 72, 80, 96])
-def test_pos_window_kernel(device, d):
+def test_pos_window_kernel(device, d, heads, monkeypatch):
+    # heads: the window kernel's form forced through FRA_WINDOW_HEADS (None:
+    # the planner's, one head per workgroup for these few pairs)
+    if heads is not None:
+        monkeypatch.setenv("FRA_WINDOW_HEADS", str(heads))
     _check([64, 64, 17, 0, 33, 64, 5, 64], 4, d, 10 + d, device)
 
 
