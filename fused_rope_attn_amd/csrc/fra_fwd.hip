@@ -42,15 +42,27 @@ int fail(int code, const char *fmt, ...) {
 // blocks per segment, 16 x 80 heads).  Each part
 // writes its unnormalised rows, running max and row sum to the workspace;
 // split_merge_kernel, the next launch on the stream, combines them.
+//
+// The grid has max_seqlen's query blocks for every (segment, head); in a
+// layer of unequal segments the blocks past a shorter segment's end exit at
+// once, so the rounds are counted from a bound on the blocks that hold
+// queries: per head at most ceil(total / 256) + num_seqs.  Layers of equal
+// segments (and single segments) meet the bound and plan as before; for the
+// six unequal images of a ragged layer (10493 tokens, 16 heads) it is 752 of
+// 1056 units, no split, and the call 2.6% faster than with the split that
+// the full count asked for (its parts were mostly empty blocks).
 struct SplitPlan {
     int64_t units;  // units split (the last round)
     int parts;      // parts per unit (1: no split)
     int64_t bytes;
 };
-SplitPlan split_plan(int64_t units, int max_seqlen, int d) {
+SplitPlan split_plan(int64_t units, const fra_fwd_args *a) {
     SplitPlan sp = {0, 1, 0};
     const int64_t slots = device_cus();
     if (units <= 0) return sp;
+    const int d = a->head_dim, max_seqlen = a->max_seqlen;
+    const int64_t bound = (int64_t)a->num_heads * (((int64_t)a->total_seq + kLongBQ - 1) / kLongBQ + a->num_seqs);
+    units = std::min(units, bound);
     const int64_t rounds = (units + slots - 1) / slots;
     const int64_t tail = units - (rounds - 1) * slots;
     int parts = (int)std::min<int64_t>(slots / tail, kSplitMaxParts);
@@ -257,7 +269,7 @@ int plan(const fra_fwd_args *a, Choice &c, KParams &kp, bool allow_pre = true,
     } else {
         kp.qblocks = (a->max_seqlen + kLongBQ - 1) / kLongBQ;
         const int64_t units = sh * kp.qblocks;
-        const SplitPlan sp = split_plan(units, a->max_seqlen, d);
+        const SplitPlan sp = split_plan(units, a);
         kp.tail_first = (int32_t)std::min<int64_t>(units, 0x7fffffff);
         kp.tail_split = 1;
         // Workspace: [k_rot rows | split scratch].  With room for k_rot the
@@ -391,7 +403,7 @@ int fra_fwd_varlen_static(const fra_fwd_args *args, void *stream) {
     int rc = plan(&a, c, kp, false);
     if (rc != FRA_OK) return rc;
     if (c.kernel == FRA_KERNEL_LONG) {
-        const SplitPlan sp = split_plan((int64_t)a.num_seqs * a.num_heads * kp.qblocks, a.max_seqlen, a.head_dim);
+        const SplitPlan sp = split_plan((int64_t)a.num_seqs * a.num_heads * kp.qblocks, &a);
         if (sp.parts > 1) {
             if (sp.bytes > kStaticScratchBytes)
                 return fail(FRA_EUNSUPPORTED,
@@ -447,7 +459,7 @@ int workspace_bytes(const fra_fwd_args *args, const fra_rope_positions *rope, in
     const int rc = plan(&a, c, kp, true, rope);
     if (rc != FRA_OK) return rc;
     if (c.kernel == FRA_KERNEL_LONG) {
-        const SplitPlan sp = split_plan((int64_t)a.num_seqs * a.num_heads * kp.qblocks, a.max_seqlen, a.head_dim);
+        const SplitPlan sp = split_plan((int64_t)a.num_seqs * a.num_heads * kp.qblocks, &a);
         *bytes = krot_workspace_bytes(&a) + (sp.parts > 1 ? sp.bytes : 0);
     }
     g_err[0] = 0;

@@ -177,6 +177,27 @@ def test_forward_workspace_size_and_alignment():
     assert "workspace" in lib.fra_last_error().decode()
 
 
+@pytest.mark.parametrize("total,nseg,max_seqlen,parts", [
+    # six unequal images as full-attention segments (10493 tokens): the grid
+    # has 11 query blocks for every (segment, head), 1056 units, but at most
+    # 16 x (41 + 6) = 752 hold queries -- three rounds, no split
+    (10493, 6, 2736, 0),
+    # the same segment count with every segment full: 1056 real units, the
+    # last round of 32 split in 5 parts (43 key blocks, at least 8 a part)
+    (6 * 2736, 6, 2736, 5),
+])
+def test_split_plan_counts_query_blocks_that_exist(total, nseg, max_seqlen, parts):
+    lib = _lib.load()
+    a = make_args(n=total, nseg=nseg, max_seqlen=max_seqlen, num_seqs=nseg)
+    nbytes = ctypes.c_int64(0)
+    assert lib.fra_workspace_bytes(a, ctypes.byref(nbytes)) == _lib.FRA_OK
+    a.workspace, a.workspace_bytes = (1 << 20) * 10, nbytes.value
+    rc, p = plan_of(a)
+    assert rc == _lib.FRA_OK and p.kernel == _lib.FRA_KERNEL_LONG
+    assert p.split_parts == parts
+    assert p.grid >= 16 * nseg * (-(-max_seqlen // 256))
+
+
 @pytest.mark.parametrize("seglen,nseg,parts", [
     (9216, 1, 4),   # 576 units: a last round of 64 on 256 CUs, 144 key blocks per unit
     (2304, 8, 2),   # 1152 units: 128 left over, 2 parts of 18 key blocks
