@@ -20,6 +20,7 @@ records an autograd graph when q, k or v require grad, and
 ``fused_rope_attention_fwd`` / ``fused_rope_attention_bwd`` expose the
 forward with its log-sum-exp and the gradients as plain functions.
 """
+import contextlib
 import ctypes
 from collections import OrderedDict
 
@@ -137,6 +138,26 @@ def _fits(t: torch.Tensor, ptr_align: int, stride_mult: int) -> bool:
     if t.data_ptr() % ptr_align:
         return False
     return all(s % stride_mult == 0 for s in t.stride()[:-1])
+
+
+# The current stream of a device as a raw handle, without building a
+# torch.cuda.Stream object per call (torch's own generated code reads it the
+# same way); the public call where this build of torch lacks the binding.
+_get_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _raw_stream(device: torch.device) -> int:
+    if _get_raw_stream is not None:
+        return _get_raw_stream(device.index)
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _on_device(device: torch.device):
+    """``device`` current for the launch (the library queries the current
+    device's CU count); no context switch when it already is."""
+    if device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 def _kernel_layout(t: torch.Tensor, ptr_align: int, stride_mult: int) -> torch.Tensor:
@@ -435,17 +456,17 @@ def _forward(q, k, v, cos, sin, cu, max_seqlen: int, scale: float, out, lse, row
     if lse is not None:
         args.lse = lse.data_ptr()
     ws = None
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         # The long kernel's workspace (scratch, per call, from torch's
         # caching allocator: stream-ordered reuse keeps it alive for the
         # kernels that use it) holds K rotated once per call and, where a
         # partly filled last round of workgroups is split along the key
-        # range, the parts' partial rows.
-        nbytes = _workspace_bytes(lib, args)
+        # range, the parts' partial rows.  The window kernel takes none.
+        nbytes = _workspace_bytes(lib, args) if _uses_long_kernel(max_seqlen, d) else 0
         if nbytes:
             ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
             args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
-        stream = torch.cuda.current_stream(q.device).cuda_stream
+        stream = _raw_stream(q.device)
         if rows is not None:
             _lib.check(lib.fra_fwd_varlen_gather(args, None, rows.data_ptr(), stream))
         else:
@@ -542,12 +563,12 @@ def _backward(dout, q, k, v, cos, sin, out, lse, cu, max_seqlen: int, scale: flo
     lib = _lib.load()
     dsts = [t if _fits(t, 16, 8) else torch.empty(q.shape, dtype=q.dtype, device=q.device) for t in (dq, dk, dv)]
     a, _keep = _bwd_args(dout, q, k, v, cos, sin, out, lse, cu, max_seqlen, scale, *dsts)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         nbytes = ctypes.c_int64(0)
         _lib.check(lib.fra_bwd_workspace_bytes(a, ctypes.byref(nbytes)))
         ws = torch.empty(max(int(nbytes.value), 16), dtype=torch.uint8, device=q.device)
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-        _lib.check(lib.fra_bwd_varlen(a, torch.cuda.current_stream(q.device).cuda_stream))
+        _lib.check(lib.fra_bwd_varlen(a, _raw_stream(q.device)))
     for dst, t in zip(dsts, (dq, dk, dv)):
         if dst is not t:
             t.copy_(dst)
@@ -815,13 +836,13 @@ def fused_rope_attention_pos(
     a, rope, _keep = _pos_args(q, k, v, pos, inv_freq, dst, cu, max_seqlen, scale)
     lib = _lib.load()
     ws = None
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         nbytes = ctypes.c_int64(0)
         _lib.check(lib.fra_workspace_bytes_pos(a, rope, ctypes.byref(nbytes)))
         if nbytes.value:
             ws = torch.empty(int(nbytes.value), dtype=torch.uint8, device=q.device)
             a.workspace, a.workspace_bytes = ws.data_ptr(), int(nbytes.value)
-        stream = torch.cuda.current_stream(q.device).cuda_stream
+        stream = _raw_stream(q.device)
         if rows is not None:
             if _uses_long_kernel(max_seqlen, q.shape[2]):
                 raise ValueError(f"row_index is for window layers (segments of at most 64 tokens, head_dim <= "
