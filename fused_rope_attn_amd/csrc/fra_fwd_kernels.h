@@ -1304,6 +1304,44 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         }
     };
 
+    // The matrix half of a ping-pong iteration: O^T += V(x)^T P^T (x = V
+    // buffer parity) and S^T of the block in K_rot buffer x ^ 1, as one stream
+    // of 4 NDT + 2 S MFMAs whose LDS operands are read kLookahead MFMAs ahead
+    // (at most 14 LDS reads in flight, within the 4-bit LGKM counter), so that
+    // the read latency hides behind the matrix core instead of stalling each
+    // MFMA on its own operand.
+    auto matrix_half = [&](int x, const u32x4 (&pop)[4], f32x16 (&nxt)[2]) {
+        constexpr int NV = 4 * NDT, NOPS = NV + 2 * S, kLookahead = 7;
+        const char *vb = lds + v_lane + x * LDS::kV;
+        const char *kb = lds + k_lane + (x ^ 1) * LDS::kKrot;
+        u32x4 op[NOPS];
+        auto rd = [&](int i) {
+            if (i < NV) {
+                const char *cp = vb + 16 * (i / NDT) * (VPC * 16) + 64 * (i % NDT);
+                const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)cp);
+                const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)(cp + 8 * (VPC * 16)));
+                const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+                op[i] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+            } else {
+                const int k = i - NV;
+                op[i] = *(const u32x4 *)(kb + (k & 1) * (32 * KS * 2) + 32 * (k >> 1));
+            }
+        };
+#pragma unroll
+        for (int i = 0; i < kLookahead && i < NOPS; ++i) rd(i);
+#pragma unroll
+        for (int i = 0; i < NOPS; ++i) {
+            if (i + kLookahead < NOPS) rd(i + kLookahead);
+            if (i < NV) {
+                oacc[i % NDT] = E::mma(op[i], pop[i / NDT], oacc[i % NDT]);
+            } else {
+                const int k = i - NV, ac = k & 1, tt = k >> 1;
+                nxt[ac] = E::mma(op[i], qop[tt], tt == 0 ? f32x16{} : nxt[ac]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
     f32x16 sA[2], sB[2];
     qk(0, sA);
     wait_dma();
@@ -1432,18 +1470,25 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
         }
         if constexpr (PRE) {
             // Ping-pong: wavefronts 0-3 and 4-7 (one of each per SIMD) run
-            // half an iteration apart, with a barrier per half-iteration, so
-            // that one wavefront of a SIMD does phase A (QK^T MFMAs beside
-            // the exponentials) while the other does phase B (the PV MFMAs).
-            // Group 0 runs A(j) in half-iteration 2j and B(j) in 2j + 1;
-            // group 1 one half later.  Every wavefront issues its K_rot(j+2)
-            // jobs at the start of half-iteration 2j (K_rot(j)'s buffer was
-            // last read in 2j - 1) and its V(j+1) jobs at the start of 2j + 1
-            // (V(j-1)'s buffer was last read in 2j), and ends each
-            // half-iteration waiting for the jobs it issued in the one
-            // before: what a half-iteration reads was loaded two halves
-            // earlier and is behind a barrier.  Block j + 2 of the last
-            // steady iteration's K_rot jobs is the generic loop's.
+            // half an iteration apart, with a barrier per half-iteration.  A
+            // wavefront's iteration j is a vector half, the softmax of S(j)
+            // (row max, lazy rescale, exponentials, P(j) packed), and a matrix
+            // half, O += V(j)^T P(j)^T and S(j+1) = K_rot(j+1) Q_rot^T: 22
+            // MFMAs with only their LDS operand reads beside them.  While one
+            // wavefront of a SIMD feeds the matrix core, the other runs its
+            // exponentials on the vector unit; no wavefront's in-order issue
+            // holds vector work behind an MFMA that waits for the matrix core.
+            // Group 0 runs the vector half of j in half-iteration 2j and the
+            // matrix half in 2j + 1; group 1 one half later.  Every wavefront
+            // issues its K_rot(j+2) jobs at the start of half-iteration 2j + 1
+            // (the buffer last held K_rot(j), whose last reader, group 1's
+            // matrix half of j - 1, ran in 2j) and its V(j+1) jobs at the start
+            // of 2j + 2 (V(j-1)'s buffer, last read in 2j); the first reader of
+            // both (group 0's matrix half of j + 1) runs in 2j + 3.  A half
+            // ends with a barrier after the V jobs issued at its start have
+            // landed (the K_rot jobs may stay in flight for one more half).
+            // The two kinds go in different halves because a burst of direct
+            // loads stalls the issuing wavefronts on the CU's memory path.
             static_assert(kLongWaves == 8, "two groups of one wavefront per SIMD");
             const int grp = w >> 2;
             // s_waitcnt takes an immediate; more outstanding jobs than the
@@ -1454,40 +1499,73 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
                 else if (keep == 2) asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
                 else asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
             };
-            auto issue = [&](bool kind, int par) {  // this wavefront's jobs of one kind, buffer parity par
-#pragma unroll
-                for (int m = 0; m < MPER; ++m) {
-                    if (has_job(m) && kjob[m] == kind) {
-                        if (jvoff[m] != kPadSlot) dma16(jptr[m] + jvoff[m], lds_addr(par ? +jdst[m][1] : +jdst[m][0]));
-                        jptr[m] += jstep[m];
-                    }
+            // Job m of this wavefront for iteration parity P (K_rot(j+2) or
+            // V(j+1)).
+            auto issue_job = [&](int m, int par) {
+                if (has_job(m)) {
+                    if (jvoff[m] != kPadSlot) dma16(jptr[m] + jvoff[m], lds_addr(par ? +jdst[m][1] : +jdst[m][0]));
+                    jptr[m] += jstep[m];
                 }
             };
-            auto iteration_pp = [&](auto par_tag, int jj, f32x16 (&cur)[2], f32x16 (&nxt)[2], bool more) {
-                constexpr int P = decltype(par_tag)::value;
-                u32x4 pop[4];
-                issue(grp == 0, P);  // group 0: K_rot(jj+2); group 1: V(jj+1)
-                phase_a(jj, cur, nxt, pop);
-                half_barrier(grp == 0 ? nk : nv);
-                if (grp == 0) issue(false, P);      // V(jj+1)
-                else if (more) issue(true, P ^ 1);  // K_rot(jj+3)
-                pv(jj, pop);
-                // Row max of S(jj+1) (a full block) beside the PV MFMAs, whose
-                // VALU slots are otherwise empty; a rescale of O waits for
-                // them, which it must (O then holds block jj).
-                smax(nxt, kLongBKV);
-                half_barrier(grp == 0 ? nv : (more ? nk : 0));
+            auto issue = [&](bool kind, int par) {  // this wavefront's jobs of one kind
+#pragma unroll
+                for (int m = 0; m < MPER; ++m)
+                    if (kjob[m] == kind) issue_job(m, par);
             };
-            smax(sA, kLongBKV);  // S(0), a full block
-            if (grp == 1) {  // K_rot(2), which group 0 issues with A(0)
-                issue(true, 0);
-                half_barrier(nk);
-            }
+            // Softmax of S(j) into the PV operands, the exponentials in eight
+            // groups of four.
+            auto vector_half = [&](f32x16 (&cur)[2], u32x4 (&pop)[4]) {
+                smax(cur, kLongBKV);
+                float lsum = 0.f;
+#pragma unroll
+                for (int g8 = 0; g8 < 8; ++g8) {
+#pragma unroll
+                    for (int e = 4 * g8; e < 4 * g8 + 4; ++e) {
+                        const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(cur[e >> 4][e & 15], sl, -m_i));
+                        cur[e >> 4][e & 15] = x;
+                        if constexpr (!ONES) lsum += x;
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if constexpr (!ONES) l_i += sum_pair32(lsum);
+#pragma unroll
+                for (int a = 0; a < 2; ++a) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        pop[2 * a + h] = u32x4{E::pack(cur[a][8 * h + 0], cur[a][8 * h + 1]),
+                                               E::pack(cur[a][8 * h + 2], cur[a][8 * h + 3]),
+                                               E::pack(cur[a][8 * h + 4], cur[a][8 * h + 5]),
+                                               E::pack(cur[a][8 * h + 6], cur[a][8 * h + 7])};
+                }
+                // P(j) is complete here.  Without the pin the compiler sinks
+                // the exponentials and packs to their use, past the barrier
+                // into the matrix half.
+#pragma unroll
+                for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(pop[i]));
+            };
+            auto iteration_pp = [&](auto par_tag, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+                constexpr int P = decltype(par_tag)::value;  // parity of j
+                u32x4 pop[4];
+                if (grp == 0) {
+                    vector_half(cur, pop);
+                    half_barrier(0);
+                }
+                issue(true, P);  // K_rot(j+2)
+                if (grp != 0) {
+                    vector_half(cur, pop);
+                    half_barrier(nk);
+                    issue(false, P);  // V(j+1)
+                }
+                matrix_half(P, pop, nxt);
+                half_barrier(grp == 0 ? nk : 0);
+                if (grp == 0) issue(false, P);  // V(j+1), at the start of the next half
+            };
+            if (grp == 1) half_barrier(0);  // group 0's vector half of S(0)
             for (; j + 1 < nsteady; j += 2) {
-                iteration_pp(Even{}, j, sA, sB, true);
-                iteration_pp(Odd{}, j + 1, sB, sA, j + 3 < nsteady);
+                iteration_pp(Even{}, sA, sB);
+                iteration_pp(Odd{}, sB, sA);
             }
-            if (grp == 0) half_barrier(0);  // group 1 finishes B of the last steady iteration
+            if (grp == 0) half_barrier(0);  // group 1 finishes the matrix half of the last steady iteration
         } else {
             for (; j + 1 < nsteady; j += 2) {
                 iteration_steady(Even{}, j, sA, sB);
