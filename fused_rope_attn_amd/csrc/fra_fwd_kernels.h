@@ -868,6 +868,25 @@ __global__ __launch_bounds__(256) void split_merge_kernel(const KParams p) {
         u32x2{E::pack(acc1[0] * inv, acc1[1] * inv), E::pack(acc1[2] * inv, acc1[3] * inv)};
 }
 
+// Read schedule of the long kernel's matrix half: NOPS MFMA operands, the
+// first NV of them two LDS reads each (transposed V), the rest one.  v[i] is
+// the number of operands read by the time MFMA i issues: as many as keep at
+// most kLimit reads in flight, the most the 4-bit LGKM counter tracks.
+template <int NV, int NOPS> struct MatrixReads {
+    static constexpr int kLimit = 15;
+    int v[NOPS];
+    static constexpr MatrixReads make() {
+        MatrixReads f{};
+        int nx = 0, fl = 0;
+        for (int i = 0; i < NOPS; ++i) {
+            while (nx < NOPS && fl + (nx < NV ? 2 : 1) <= kLimit) fl += nx++ < NV ? 2 : 1;
+            f.v[i] = nx;
+            fl -= i < NV ? 2 : 1;  // MFMA i waits for its operand
+        }
+        return f;
+    }
+};
+
 template <int D, class E, int RD, bool FULL, bool PRE>
 __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) {
     using LDS = LongLds<D, RD, FULL, PRE>;
@@ -1306,12 +1325,12 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
 
     // The matrix half of a ping-pong iteration: O^T += V(x)^T P^T (x = V
     // buffer parity) and S^T of the block in K_rot buffer x ^ 1, as one stream
-    // of 4 NDT + 2 S MFMAs whose LDS operands are read kLookahead MFMAs ahead
-    // (at most 14 LDS reads in flight, within the 4-bit LGKM counter), so that
-    // the read latency hides behind the matrix core instead of stalling each
-    // MFMA on its own operand.
+    // of 4 NDT + 2 S MFMAs whose LDS operands are read as far ahead as the
+    // LGKM counter allows (MatrixReads), so that the read latency hides
+    // behind the matrix core instead of stalling each MFMA on its operand.
     auto matrix_half = [&](int x, const u32x4 (&pop)[4], f32x16 (&nxt)[2]) {
-        constexpr int NV = 4 * NDT, NOPS = NV + 2 * S, kLookahead = 7;
+        constexpr int NV = 4 * NDT, NOPS = NV + 2 * S;
+        constexpr MatrixReads<NV, NOPS> plan = MatrixReads<NV, NOPS>::make();
         const char *vb = lds + v_lane + x * LDS::kV;
         const char *kb = lds + k_lane + (x ^ 1) * LDS::kKrot;
         u32x4 op[NOPS];
@@ -1328,10 +1347,9 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
             }
         };
 #pragma unroll
-        for (int i = 0; i < kLookahead && i < NOPS; ++i) rd(i);
-#pragma unroll
         for (int i = 0; i < NOPS; ++i) {
-            if (i + kLookahead < NOPS) rd(i + kLookahead);
+#pragma unroll
+            for (int k = i == 0 ? 0 : plan.v[i - 1]; k < plan.v[i]; ++k) rd(k);
             if (i < NV) {
                 oacc[i % NDT] = E::mma(op[i], pop[i / NDT], oacc[i % NDT]);
             } else {
