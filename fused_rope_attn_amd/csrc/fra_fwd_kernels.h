@@ -1561,14 +1561,14 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
 #pragma unroll
                 for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(pop[i]));
             };
-            auto iteration_pp = [&](auto par_tag, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+            auto iteration_pp = [&](auto par_tag, f32x16 (&cur)[2], f32x16 (&nxt)[2], bool kmore) {
                 constexpr int P = decltype(par_tag)::value;  // parity of j
                 u32x4 pop[4];
                 if (grp == 0) {
                     vector_half(cur, pop);
                     half_barrier(0);
                 }
-                issue(true, P);  // K_rot(j+2)
+                if (kmore) issue(true, P);  // K_rot(j+2), where that block exists
                 if (grp != 0) {
                     vector_half(cur, pop);
                     half_barrier(nk);
@@ -1578,10 +1578,19 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
                 half_barrier(grp == 0 ? nk : 0);
                 if (grp == 0) issue(false, P);  // V(j+1), at the start of the next half
             };
+            // With a full last block the loop runs through j = nblk - 2 (its
+            // last K_rot loads are skipped: those blocks do not exist), and
+            // only the last block takes the generic path.  (A partial last
+            // block is loaded by the generic path, which clamps its rows.)
+            const int npp = Lkv % kLongBKV == 0 ? nblk - 1 : nsteady;
             if (grp == 1) half_barrier(0);  // group 0's vector half of S(0)
-            for (; j + 1 < nsteady; j += 2) {
-                iteration_pp(Even{}, sA, sB);
-                iteration_pp(Odd{}, sB, sA);
+            for (; j + 1 < npp; j += 2) {
+                iteration_pp(Even{}, sA, sB, j + 2 < nblk);
+                iteration_pp(Odd{}, sB, sA, j + 3 < nblk);
+            }
+            if (j < npp) {  // an odd count: one more, j even
+                iteration_pp(Even{}, sA, sB, j + 2 < nblk);
+                ++j;
             }
             if (grp == 0) half_barrier(0);  // group 1 finishes the matrix half of the last steady iteration
         } else {
@@ -1590,6 +1599,11 @@ __global__ __launch_bounds__(kLongThreads, 1) void long_kernel(const KParams p) 
                 iteration_steady(Odd{}, j + 1, sB, sA);
             }
         }
+    }
+    // S(j) is in sA for even j, in sB for odd j.
+    if ((j & 1) && j < nblk) {
+        iteration_generic(j, sB, sA);
+        ++j;
     }
     for (; j < nblk; j += 2) {
         iteration_generic(j, sA, sB);
