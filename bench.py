@@ -658,7 +658,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the op shards by head or "
-              "segment with no exchange; see DESIGN.md).  Run with --gpus 1.", file=sys.stderr)
+              "segment with no exchange between GPUs).  Run with --gpus 1.", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
