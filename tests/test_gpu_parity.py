@@ -126,6 +126,20 @@ def test_long_kernel_ragged(device, d, li):
     assert_close(out, oracle(case, "bf16"), EMU_MAX_ABS, EMU_MEAN_ABS, f"long d={d} lens={lens} (emulated)")
 
 
+@pytest.mark.parametrize("d", [72, 80])
+@pytest.mark.parametrize("lens", [[320, 384], [448, 512], [1024, 321], [383, 640]])
+def test_long_kernel_block_counts(device, d, lens):
+    """Segments of 5 to 16 key blocks, full or partial last block: the
+    steady loop runs through the second-to-last block when the last one is
+    full (an even or odd number of its iterations), else stops three
+    blocks earlier, and the generic loop takes the rest."""
+    case = random_case(lens, h=2, d=d, seed=1500 + sum(lens) + d)
+    print(f"long block counts lens={lens} head_dim={d}", flush=True)
+    assert plan(*(case[k].to(device) for k in ("q", "k", "v", "cos", "sin", "cu_seqlens")),
+                case["max_seqlen"])["kernel"] == "long"
+    assert_close(f32(run_gpu(case, device)), oracle(case), MAX_ABS, MEAN_ABS, f"lens={lens} d={d}")
+
+
 @pytest.mark.parametrize("d", [72, 80, 96, 128])
 @pytest.mark.parametrize("rope_dtype", [torch.float32, torch.bfloat16])
 def test_long_kernel_full_width_tables(device, d, rope_dtype):
